@@ -1,0 +1,158 @@
+/*
+ * stquant_hip.h -- C ABI of the MI355X-native fused MDQ AdamW step.
+ *
+ * The shared library stream-mm2026_amd/mdq_hip/libstquant_hip.so exports
+ * these symbols.  Signatures carry plain pointers, sizes and dtype codes only;
+ * every device pointer must address memory of the current HIP device, and
+ * every call is asynchronous on the given hipStream_t (NULL = the null stream).
+ *
+ * Return value: STQ_OK, or an STQ_ERR_* code with a message available from
+ * stq_last_error() (thread-local).  Argument errors are reported before any
+ * device work is queued.
+ */
+#ifndef STQUANT_HIP_H
+#define STQUANT_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define STQ_ABI_VERSION 1
+
+enum stq_status {
+    STQ_OK = 0,
+    STQ_ERR_INVALID = 1, /* bad argument; nothing was launched            */
+    STQ_ERR_HIP = 2      /* HIP runtime error while queueing device work  */
+};
+
+/* Element types, named as torch names them in error messages. */
+enum stq_dtype {
+    STQ_FLOAT = 0,    /* float32  ("Float")    */
+    STQ_BFLOAT16 = 1, /* bfloat16 ("BFloat16") */
+    STQ_HALF = 2,     /* float16  ("Half")     */
+    STQ_BYTE = 3,     /* uint8    ("Byte")     */
+    STQ_CHAR = 4,     /* int8     ("Char")     */
+    STQ_SHORT = 5,    /* int16    ("Short")    */
+    STQ_UINT16 = 6,   /* uint16   ("UInt16")   */
+    STQ_INT = 7,      /* int32    ("Int")      */
+    STQ_UINT32 = 8,   /* uint32   ("UInt32")   */
+    STQ_LONG = 9      /* int64    ("Long")     */
+};
+
+enum stq_rounding {
+    STQ_ROUND_NEAREST = 0,    /* round half away from zero (the reference) */
+    STQ_ROUND_STOCHASTIC = 1  /* floor(x + u), u from Philox4x32-10 (codes <= 16 bits) */
+};
+
+/*
+ * One fused dequant -> AdamW -> requant step on one parameter tensor.
+ *
+ * Replaces launch_fused_mdq_adamw (/root/reference/CUDA/stquant_kernel.cu:414-465),
+ * which the reference binds to Python as stquant_timetest_cpp.fused_mdq_adamw
+ * (/root/reference/CUDA/stquant_core.cpp:3-14).  Same arguments in the same
+ * order, each torch::Tensor split into (pointer, dtype, numel):
+ *
+ *   p           float32[numel], updated in place
+ *   grad        float32 (the reference) or bfloat16 / float16 [numel], read only
+ *   exp_avg     m codes: uint8 packed nibbles (bits == 4, exp_avg_sq_numel == 0),
+ *               else int8 / int16 / int32 [numel]
+ *   exp_avg_sq  v codes: empty (packed) or uint8 / uint16 / uint32 [numel]
+ *   scale_m, scale_v, v_min   float32[ceil(numel / B)], B = min(block_size, 1024)
+ *   beta1 .. eps              AdamW hyper-parameters (fp32)
+ *   step        the tensor's step count, already incremented (>= 1)
+ *   bits        code width: 4 for packed nibbles, 1..8 / 1..16 / 1..32 otherwise
+ *   block_size  quant block size; min(block_size, 1024) must be a power of two
+ *   profile_cycles  NULL (profile_numel == 0) or int64[>= 5] device buffer that
+ *               receives += clock64 cycles of the dequant / adam_mv /
+ *               scale_reduce / quant / update_p phases
+ *
+ * Extensions beyond the reference: grad dtype, rounding / seed / tensor_id
+ * (stochastic rounding stream), the stream argument, and 64-bit numel.
+ * Storage dispatch and its error message follow stquant_kernel.cu:430-464.
+ */
+int stq_fused_mdq_adamw(float *p, const void *grad, int grad_dtype, int64_t grad_numel,
+                        int64_t numel,
+                        void *exp_avg, int exp_avg_dtype, int64_t exp_avg_numel,
+                        void *exp_avg_sq, int exp_avg_sq_dtype, int64_t exp_avg_sq_numel,
+                        float *scale_m, int64_t scale_m_numel,
+                        float *scale_v, int64_t scale_v_numel,
+                        float *v_min, int64_t v_min_numel,
+                        float beta1, float beta2, float lr, float weight_decay, float eps,
+                        int step, int bits, int block_size,
+                        int64_t *profile_cycles, int64_t profile_numel,
+                        int rounding, uint64_t seed, uint32_t tensor_id,
+                        void *stream);
+
+/* One tensor of a multi-tensor step; fields as in stq_fused_mdq_adamw. */
+typedef struct stq_tensor {
+    float *p;
+    const void *grad;
+    void *exp_avg;
+    void *exp_avg_sq;
+    float *scale_m;
+    float *scale_v;
+    float *v_min;
+    int64_t numel;
+    int64_t grad_numel;
+    int64_t exp_avg_numel;
+    int64_t exp_avg_sq_numel;
+    int64_t scale_m_numel;
+    int64_t scale_v_numel;
+    int64_t v_min_numel;
+    float beta1, beta2, lr, weight_decay, eps;
+    int32_t step;
+    int32_t bits;
+    uint32_t tensor_id;
+} stq_tensor;
+
+/*
+ * Multi-tensor apply: one kernel launch walks all n_tensors tensors from one
+ * packed metadata buffer.  Per-element results are identical to calling
+ * stq_fused_mdq_adamw once per tensor.  All tensors share the storage dtype
+ * pair, the grad dtype, the block size and the rounding mode; step, bits and
+ * the AdamW hyper-parameters are per tensor.
+ *
+ * No reference counterpart as one call: it replaces the per-tensor launch loop
+ * of MDQAdamWSimple.step (/root/reference/CUDA/stquant_opt_simple.py:501-502
+ * -> :246-263) and MDQAdamWSimpleFusedIO (/root/reference/CUDA/stquant_opt_fused_io.py:60-77).
+ */
+int stq_multi_tensor_mdq_adamw(const stq_tensor *tensors, int n_tensors,
+                               int grad_dtype, int exp_avg_dtype, int exp_avg_sq_dtype,
+                               int block_size, int rounding, uint64_t seed,
+                               int64_t *profile_cycles, int64_t profile_numel,
+                               void *stream);
+
+/* Last error message of this thread ("" when none). */
+const char *stq_last_error(void);
+
+/* STQ_ABI_VERSION of the loaded library. */
+int stq_abi_version(void);
+
+/*
+ * Device copies of the step's fp32 math, for checking it against a CPU
+ * implementation (no reference counterpart: the reference calls CUDA libm).
+ *   which = 0: e^x, 1: log x (x a positive normal, +inf or NaN).
+ * stq_device_math: y[i] = f(x[i]) for device arrays x, y of n floats.
+ * stq_device_math_digests: for the bit patterns first .. first+count-1, the
+ *   sum over each chunk of mix64(bits(x) << 32 | bits(f(x))) into
+ *   digests[ceil(count / chunk)] (device uint64, zeroed by the caller).
+ */
+int stq_device_math(int which, const float *x, float *y, int64_t n, void *stream);
+int stq_device_math_digests(int which, uint32_t first, uint32_t count, uint32_t chunk,
+                            uint64_t *digests, void *stream);
+
+/* Host (CPU) builds of the same inline functions the kernels use. */
+void stq_host_math(int which, const float *x, float *y, int64_t n);
+/* out[i] = round-half-away(u[i] / d[i]) via the kernel's fp32 fma method,
+ * with the reciprocal of d perturbed by inv_ulps units in the last place
+ * (the device uses a hardware reciprocal within 1 ulp). */
+void stq_host_round_half_away(const float *u, const float *d, float *out, int64_t n, int inv_ulps);
+void stq_host_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* STQUANT_HIP_H */

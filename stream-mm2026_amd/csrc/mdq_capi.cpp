@@ -1,0 +1,425 @@
+// mdq_capi.cpp -- C ABI of the fused MDQ AdamW step (declared in
+// include/stquant_hip.h): argument checks, per-tensor AdamW constants,
+// descriptor packing/upload and kernel dispatch.
+//
+// Replaces launch_fused_mdq_adamw (/root/reference/CUDA/stquant_kernel.cu:414-465)
+// and its pybind shim (/root/reference/CUDA/stquant_core.cpp:3-14).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "../../include/stquant_hip.h"
+#include "mdq_desc.h"
+#include "mdq_launch.h"
+#include "mdq_math.h"
+
+namespace {
+
+using mdq::MdqDesc;
+
+thread_local std::string g_err;
+
+int fail(int code, const char *fmt, ...)
+{
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char *what)
+{
+    return fail(STQ_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+const char *dtype_name(int dt)
+{
+    switch (dt) {
+    case STQ_FLOAT: return "Float";
+    case STQ_BFLOAT16: return "BFloat16";
+    case STQ_HALF: return "Half";
+    case STQ_BYTE: return "Byte";
+    case STQ_CHAR: return "Char";
+    case STQ_SHORT: return "Short";
+    case STQ_UINT16: return "UInt16";
+    case STQ_INT: return "Int";
+    case STQ_UINT32: return "UInt32";
+    case STQ_LONG: return "Long";
+    default: return "Unknown";
+    }
+}
+
+int elem_bytes(int dt)
+{
+    switch (dt) {
+    case STQ_FLOAT: case STQ_INT: case STQ_UINT32: return 4;
+    case STQ_BFLOAT16: case STQ_HALF: case STQ_SHORT: case STQ_UINT16: return 2;
+    case STQ_BYTE: case STQ_CHAR: return 1;
+    case STQ_LONG: return 8;
+    default: return 0;
+    }
+}
+
+// Storage dispatch of stquant_kernel.cu:430-464.  Returns the storage class or
+// -1 (message set).  packed4 needs bits == 4, uint8 m codes, empty v codes.
+int pick_storage(int bits, int ea_dt, int64_t ea_numel, int easq_dt, int64_t easq_numel, int64_t numel)
+{
+    if (bits == 4 && ea_dt == STQ_BYTE && easq_numel == 0) {
+        if (ea_numel != numel) {
+            fail(STQ_ERR_INVALID, "packed4: exp_avg numel must match parameters");
+            return -1;
+        }
+        return mdq::ST_P4;
+    }
+    if (ea_dt == STQ_CHAR && easq_dt == STQ_BYTE) return mdq::ST_S8;
+    if (ea_dt == STQ_SHORT && easq_dt == STQ_UINT16) return mdq::ST_S16;
+    if (ea_dt == STQ_INT && easq_dt == STQ_UINT32) return mdq::ST_S32;
+    fail(STQ_ERR_INVALID,
+         "MDQ: state must be packed4 (uint8+empty), (int8,uint8), (int16,uint16) or (int32,uint32), got %s / %s bits=%d",
+         dtype_name(ea_dt), dtype_name(easq_dt), bits);
+    return -1;
+}
+
+int storage_width(int st)
+{
+    switch (st) {
+    case mdq::ST_P4: return 4;
+    case mdq::ST_S8: return 8;
+    case mdq::ST_S16: return 16;
+    default: return 32;
+    }
+}
+
+int code_bytes(int st) { return st == mdq::ST_P4 ? 1 : storage_width(st) / 8; }
+
+// Elements per tile for a block size (see Cfg in mdq_kernel.h).
+int64_t tile_elems(int B) { return 256 * (B >= 8 ? 8 : B); }
+
+bool is_aligned(const void *ptr, int bytes) { return ((uintptr_t)ptr % (uintptr_t)bytes) == 0; }
+
+// Checks one tensor and fills its descriptor (tile range filled by the caller).
+int make_desc(const stq_tensor &t, int storage, int grad_dt, int B, MdqDesc &d)
+{
+    if (t.numel < 0) return fail(STQ_ERR_INVALID, "numel must be >= 0");
+    if (t.grad_numel != t.numel)
+        return fail(STQ_ERR_INVALID, "grad numel (%lld) must match parameters (%lld)",
+                    (long long)t.grad_numel, (long long)t.numel);
+    if (t.bits < 1 || t.bits > storage_width(storage))
+        return fail(STQ_ERR_INVALID, "bits=%d does not fit the %d-bit code storage", t.bits,
+                    storage_width(storage));
+    if (storage == mdq::ST_P4) {
+        if (t.exp_avg_numel != t.numel)
+            return fail(STQ_ERR_INVALID, "packed4: exp_avg numel must match parameters");
+    } else if (t.exp_avg_numel < t.numel || t.exp_avg_sq_numel < t.numel) {
+        return fail(STQ_ERR_INVALID, "exp_avg / exp_avg_sq must hold numel (%lld) codes",
+                    (long long)t.numel);
+    }
+    if (t.step < 1) return fail(STQ_ERR_INVALID, "step must be >= 1 (incremented by the caller), got %d", t.step);
+    const int64_t nb = (t.numel + B - 1) / B;
+    if (t.scale_m_numel < nb || t.scale_v_numel < nb || t.v_min_numel < nb)
+        return fail(STQ_ERR_INVALID, "scale_m / scale_v / v_min need ceil(numel / %d) = %lld elements", B,
+                    (long long)nb);
+    if (t.numel > 0 && (!t.p || !t.grad || !t.exp_avg || !t.scale_m || !t.scale_v || !t.v_min ||
+                        (storage != mdq::ST_P4 && !t.exp_avg_sq)))
+        return fail(STQ_ERR_INVALID, "null data pointer");
+
+    std::memset(&d, 0, sizeof d);
+    d.p = t.p;
+    d.g = t.grad;
+    d.code_m = t.exp_avg;
+    d.code_v = storage == mdq::ST_P4 ? nullptr : t.exp_avg_sq;
+    d.scale_m = t.scale_m;
+    d.scale_v = t.scale_v;
+    d.v_min = t.v_min;
+    d.numel = t.numel;
+    // AdamW constants as stquant_kernel.cu:83-84,136-142 form them in fp32.
+    d.b1 = t.beta1;
+    d.omb1 = 1.0f - t.beta1;
+    d.b2 = t.beta2;
+    d.omb2 = 1.0f - t.beta2;
+    d.eps = t.eps;
+    const float bc1 = 1.0f - powf(t.beta1, (float)t.step);
+    const float bc2 = 1.0f - powf(t.beta2, (float)t.step);
+    d.step_size = t.lr / bc1;
+    d.inv_sqrt_bc2 = 1.0f / sqrtf(bc2);
+    d.decay = t.weight_decay != 0.0f ? 1.0f - t.lr * t.weight_decay : 1.0f;
+    d.qm = ldexpf(1.0f, t.bits - 1);
+    d.inv_qm = ldexpf(1.0f, -(t.bits - 1));
+    d.qvf = (float)(std::ldexp(1.0, t.bits) - 1.0);
+    d.qv = d.qvf;
+    d.bits = (uint32_t)t.bits;
+    d.step = (uint32_t)t.step;
+    d.tensor_id = t.tensor_id;
+    const int gb = grad_dt == STQ_FLOAT ? 4 : 2;
+    const int cb = code_bytes(storage);
+    bool al = is_aligned(t.p, 16) && is_aligned(t.grad, 4 * gb) && is_aligned(t.exp_avg, 4 * cb) &&
+              (storage == mdq::ST_P4 || is_aligned(t.exp_avg_sq, 4 * cb));
+    d.flags = al ? mdq::DF_ALIGNED : 0u;
+    return STQ_OK;
+}
+
+// ----------------------------------------------------- per-device resources
+struct Slot {
+    MdqDesc *dev = nullptr;
+    MdqDesc *host = nullptr;
+    size_t cap = 0;
+    hipEvent_t done = nullptr;
+    bool pending = false;
+};
+
+struct DevCtx {
+    std::mutex mu;
+    int cus = 0;
+    int next = 0;
+    Slot slots[8];
+};
+
+std::mutex g_ctx_mu;
+DevCtx *g_ctx[64] = {nullptr};
+
+int get_ctx(DevCtx **out)
+{
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= 64) return fail(STQ_ERR_INVALID, "device index %d out of range", dev);
+    std::lock_guard<std::mutex> lk(g_ctx_mu);
+    if (!g_ctx[dev]) {
+        DevCtx *c = new DevCtx();
+        e = hipDeviceGetAttribute(&c->cus, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) { delete c; return hip_fail(e, "hipDeviceGetAttribute"); }
+        g_ctx[dev] = c;
+    }
+    *out = g_ctx[dev];
+    return STQ_OK;
+}
+
+// Workgroups per CU of the persistent grid (env STQ_WG_PER_CU overrides).
+int wg_per_cu()
+{
+    static int v = [] {
+        const char *s = std::getenv("STQ_WG_PER_CU");
+        int x = s ? std::atoi(s) : 0;
+        return x > 0 ? x : 8;
+    }();
+    return v;
+}
+
+// Uploads descs to a device slot on `stream` and launches.  The slot's pinned
+// staging buffer is reused only after the event recorded behind its previous
+// launch has completed.
+int upload_and_launch(const std::vector<MdqDesc> &descs, int storage, int grad_dt, int log2b, bool sr,
+                      int64_t total_tiles, unsigned long long *prof, uint64_t seed, hipStream_t stream)
+{
+    DevCtx *ctx = nullptr;
+    int rc = get_ctx(&ctx);
+    if (rc != STQ_OK) return rc;
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    Slot &s = ctx->slots[ctx->next];
+    ctx->next = (ctx->next + 1) % 8;
+    hipError_t e;
+    if (s.pending) {
+        e = hipEventSynchronize(s.done);
+        if (e != hipSuccess) return hip_fail(e, "hipEventSynchronize");
+        s.pending = false;
+    }
+    const size_t need = descs.size();
+    if (s.cap < need) {
+        if (s.dev) { (void)hipFree(s.dev); s.dev = nullptr; }
+        if (s.host) { (void)hipHostFree(s.host); s.host = nullptr; }
+        s.cap = 0;
+        size_t cap = need < 64 ? 64 : need + need / 2;
+        e = hipMalloc((void **)&s.dev, cap * sizeof(MdqDesc));
+        if (e != hipSuccess) return hip_fail(e, "hipMalloc(descriptors)");
+        e = hipHostMalloc((void **)&s.host, cap * sizeof(MdqDesc), hipHostMallocDefault);
+        if (e != hipSuccess) return hip_fail(e, "hipHostMalloc(descriptors)");
+        s.cap = cap;
+    }
+    if (!s.done) {
+        e = hipEventCreateWithFlags(&s.done, hipEventDisableTiming);
+        if (e != hipSuccess) return hip_fail(e, "hipEventCreate");
+    }
+    std::memcpy(s.host, descs.data(), need * sizeof(MdqDesc));
+    e = hipMemcpyAsync(s.dev, s.host, need * sizeof(MdqDesc), hipMemcpyHostToDevice, stream);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(descriptors)");
+
+    long long cap_grid = (long long)ctx->cus * wg_per_cu();
+    int grid = (int)(total_tiles < cap_grid ? total_tiles : cap_grid);
+    const int n = (int)need;
+    switch (storage) {
+    case mdq::ST_P4: e = mdq::launch_p4(s.dev, n, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream); break;
+    case mdq::ST_S8: e = mdq::launch_s8(s.dev, n, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream); break;
+    case mdq::ST_S16: e = mdq::launch_s16(s.dev, n, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream); break;
+    default: e = mdq::launch_s32(s.dev, n, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream); break;
+    }
+    if (e != hipSuccess) return hip_fail(e, "kernel launch");
+    e = hipEventRecord(s.done, stream);
+    if (e != hipSuccess) return hip_fail(e, "hipEventRecord");
+    s.pending = true;
+    return STQ_OK;
+}
+
+int common_checks(int grad_dt, int block_size, int rounding, const int64_t *prof, int64_t prof_numel,
+                  int *log2b)
+{
+    if (grad_dt != STQ_FLOAT && grad_dt != STQ_BFLOAT16 && grad_dt != STQ_HALF)
+        return fail(STQ_ERR_INVALID, "grad must be Float, BFloat16 or Half, got %s", dtype_name(grad_dt));
+    if (block_size < 1) return fail(STQ_ERR_INVALID, "block_size must be >= 1, got %d", block_size);
+    const int B = block_size > 1024 ? 1024 : block_size;   // stquant_kernel.cu:421
+    if (B & (B - 1))
+        return fail(STQ_ERR_INVALID, "block_size must be a power of two (min(block_size, 1024) = %d)", B);
+    int l = 0;
+    while ((1 << l) < B) ++l;
+    *log2b = l;
+    if (rounding != STQ_ROUND_NEAREST && rounding != STQ_ROUND_STOCHASTIC)
+        return fail(STQ_ERR_INVALID, "rounding must be 0 (nearest) or 1 (stochastic), got %d", rounding);
+    if (prof && prof_numel < 5) return fail(STQ_ERR_INVALID, "profile_cycles needs >= 5 elements");
+    return STQ_OK;
+}
+
+int run(const stq_tensor *tensors, int n_tensors, int grad_dt, int ea_dt, int easq_dt, int block_size,
+        int rounding, uint64_t seed, int64_t *prof, int64_t prof_numel, void *stream)
+{
+    g_err.clear();
+    if (prof_numel == 0) prof = nullptr;   // empty profile buffer == off (stquant_kernel.cu:403-406)
+    int log2b = 0;
+    int rc = common_checks(grad_dt, block_size, rounding, prof, prof_numel, &log2b);
+    if (rc != STQ_OK) return rc;
+    if (n_tensors < 0 || (n_tensors > 0 && !tensors)) return fail(STQ_ERR_INVALID, "bad tensor list");
+    const int B = 1 << log2b;
+    const int64_t te = tile_elems(B);
+    std::vector<MdqDesc> descs;
+    descs.reserve((size_t)n_tensors);
+    int storage = -1;
+    int64_t tiles = 0;
+    for (int i = 0; i < n_tensors; ++i) {
+        const stq_tensor &t = tensors[i];
+        const int st = pick_storage(t.bits, ea_dt, t.exp_avg_numel, easq_dt, t.exp_avg_sq_numel, t.numel);
+        if (st < 0) return STQ_ERR_INVALID;
+        if (storage >= 0 && st != storage)
+            return fail(STQ_ERR_INVALID, "all tensors of one call must share the code storage");
+        storage = st;
+        MdqDesc d;
+        rc = make_desc(t, st, grad_dt, B, d);
+        if (rc != STQ_OK) {
+            g_err = "tensor " + std::to_string(i) + ": " + g_err;
+            return rc;
+        }
+        if (t.numel == 0) continue;
+        d.tile_begin = tiles;
+        tiles += (t.numel + te - 1) / te;
+        d.tile_end = tiles;
+        descs.push_back(d);
+    }
+    if (descs.empty()) return STQ_OK;
+    return upload_and_launch(descs, storage, grad_dt, log2b, rounding == STQ_ROUND_STOCHASTIC, tiles,
+                             reinterpret_cast<unsigned long long *>(prof), seed,
+                             reinterpret_cast<hipStream_t>(stream));
+}
+
+}  // namespace
+
+extern "C" {
+
+int stq_fused_mdq_adamw(float *p, const void *grad, int grad_dtype, int64_t grad_numel, int64_t numel,
+                        void *exp_avg, int exp_avg_dtype, int64_t exp_avg_numel,
+                        void *exp_avg_sq, int exp_avg_sq_dtype, int64_t exp_avg_sq_numel,
+                        float *scale_m, int64_t scale_m_numel, float *scale_v, int64_t scale_v_numel,
+                        float *v_min, int64_t v_min_numel,
+                        float beta1, float beta2, float lr, float weight_decay, float eps,
+                        int step, int bits, int block_size,
+                        int64_t *profile_cycles, int64_t profile_numel,
+                        int rounding, uint64_t seed, uint32_t tensor_id, void *stream)
+{
+    stq_tensor t;
+    t.p = p;
+    t.grad = grad;
+    t.exp_avg = exp_avg;
+    t.exp_avg_sq = exp_avg_sq;
+    t.scale_m = scale_m;
+    t.scale_v = scale_v;
+    t.v_min = v_min;
+    t.numel = numel;
+    t.grad_numel = grad_numel;
+    t.exp_avg_numel = exp_avg_numel;
+    t.exp_avg_sq_numel = exp_avg_sq_numel;
+    t.scale_m_numel = scale_m_numel;
+    t.scale_v_numel = scale_v_numel;
+    t.v_min_numel = v_min_numel;
+    t.beta1 = beta1;
+    t.beta2 = beta2;
+    t.lr = lr;
+    t.weight_decay = weight_decay;
+    t.eps = eps;
+    t.step = step;
+    t.bits = bits;
+    t.tensor_id = tensor_id;
+    return run(&t, 1, grad_dtype, exp_avg_dtype, exp_avg_sq_dtype, block_size, rounding, seed,
+               profile_cycles, profile_numel, stream);
+}
+
+int stq_multi_tensor_mdq_adamw(const stq_tensor *tensors, int n_tensors, int grad_dtype, int exp_avg_dtype,
+                               int exp_avg_sq_dtype, int block_size, int rounding, uint64_t seed,
+                               int64_t *profile_cycles, int64_t profile_numel, void *stream)
+{
+    return run(tensors, n_tensors, grad_dtype, exp_avg_dtype, exp_avg_sq_dtype, block_size, rounding, seed,
+               profile_cycles, profile_numel, stream);
+}
+
+const char *stq_last_error(void) { return g_err.c_str(); }
+
+int stq_abi_version(void) { return STQ_ABI_VERSION; }
+
+int stq_device_math(int which, const float *x, float *y, int64_t n, void *stream)
+{
+    g_err.clear();
+    if (which != 0 && which != 1) return fail(STQ_ERR_INVALID, "which must be 0 (exp) or 1 (log)");
+    if (n < 0 || (n > 0 && (!x || !y))) return fail(STQ_ERR_INVALID, "bad arrays");
+    hipError_t e = mdq::launch_math(which, x, y, n, reinterpret_cast<hipStream_t>(stream));
+    return e == hipSuccess ? STQ_OK : hip_fail(e, "math kernel launch");
+}
+
+int stq_device_math_digests(int which, uint32_t first, uint32_t count, uint32_t chunk, uint64_t *digests,
+                            void *stream)
+{
+    g_err.clear();
+    if (which != 0 && which != 1) return fail(STQ_ERR_INVALID, "which must be 0 (exp) or 1 (log)");
+    if (chunk == 0 || chunk % 64 != 0) return fail(STQ_ERR_INVALID, "chunk must be a positive multiple of 64");
+    if ((uint64_t)first + count > 0x100000000ull) return fail(STQ_ERR_INVALID, "range exceeds 2^32");
+    if (count > 0 && !digests) return fail(STQ_ERR_INVALID, "null digests");
+    hipError_t e = mdq::launch_math_digests(which, first, count, chunk,
+                                            reinterpret_cast<unsigned long long *>(digests),
+                                            reinterpret_cast<hipStream_t>(stream));
+    return e == hipSuccess ? STQ_OK : hip_fail(e, "math digest kernel launch");
+}
+
+void stq_host_math(int which, const float *x, float *y, int64_t n)
+{
+    for (int64_t i = 0; i < n; ++i) y[i] = which == 0 ? mdq::mdq_expf(x[i]) : mdq::mdq_logf(x[i]);
+}
+
+void stq_host_round_half_away(const float *u, const float *d, float *out, int64_t n, int inv_ulps)
+{
+    for (int64_t i = 0; i < n; ++i) {
+        const float inv = mdq::bits_f(mdq::f_bits(1.0f / d[i]) + (uint32_t)inv_ulps);
+        out[i] = mdq::mdq_round_half_away(u[i], d[i], inv, 0.5f * d[i]);
+    }
+}
+
+void stq_host_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4])
+{
+    mdq::U4 r = mdq::mdq_philox4x32_10(mdq::U4{ctr[0], ctr[1], ctr[2], ctr[3]}, key[0], key[1]);
+    out[0] = r.x; out[1] = r.y; out[2] = r.z; out[3] = r.w;
+}
+
+}  // extern "C"

@@ -1,0 +1,46 @@
+// mdq_desc.h -- per-tensor descriptor of the multi-tensor launch.
+//
+// The host launcher (mdq_capi.cpp) packs one MdqDesc per tensor into a single
+// device buffer; the kernel walks the whole param/grad/state list from it.
+// Each tensor owns the contiguous global tile range [tile_begin, tile_end);
+// a tile is 256 lanes x elements-per-lane and never straddles two tensors.
+#pragma once
+#include <stdint.h>
+
+namespace mdq {
+
+enum Storage : int { ST_P4 = 0, ST_S8 = 1, ST_S16 = 2, ST_S32 = 3 };
+enum GradType : int { GT_F32 = 0, GT_BF16 = 1, GT_F16 = 2 };
+
+enum DescFlags : uint32_t {
+    DF_ALIGNED = 1u,  // every pointer meets the 16-byte vector-access alignment
+};
+
+struct alignas(16) MdqDesc {
+    float *p;             // [numel] fp32 params, updated in place
+    const void *g;        // [numel] grads (GradType of the launch)
+    void *code_m;         // P4: packed bytes; else int8/16/32 m codes
+    void *code_v;         // P4: unused; else uint8/16/32 v codes
+    float *scale_m;       // [nblocks]
+    float *scale_v;       // [nblocks]
+    float *v_min;         // [nblocks]
+    int64_t numel;
+    int64_t tile_begin;
+    int64_t tile_end;
+    // AdamW constants of this tensor (host-computed once per step).
+    float b1, omb1, b2, omb2;
+    float eps;
+    float step_size;      // lr / (1 - beta1^t)
+    float inv_sqrt_bc2;   // 1 / sqrt(1 - beta2^t)
+    float decay;          // 1 - lr * weight_decay (1 when weight_decay == 0)
+    // Code range: m in [-qm, qm - 1], v in [0, qv]; inv_qm = 1 / qm (a power of two).
+    float qm, qv, inv_qm, qvf;  // qvf = (float)(2^bits - 1) as the reference divides by it
+    uint32_t bits;
+    uint32_t step;
+    uint32_t tensor_id;
+    uint32_t flags;
+};
+
+static_assert(sizeof(MdqDesc) % 16 == 0, "descriptor must stay 16-byte sized");
+
+}  // namespace mdq

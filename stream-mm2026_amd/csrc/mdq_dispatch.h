@@ -1,0 +1,54 @@
+// mdq_dispatch.h -- run-time (grad dtype, block size, rounding) -> template
+// instance dispatch for one storage class.  Included once per storage by
+// mdq_kernels_<storage>.hip so the four classes compile in parallel.
+#pragma once
+#include "mdq_kernel.h"
+#include "mdq_launch.h"
+
+namespace mdq {
+
+template <int ST, int GT, int LOG2B, bool SR>
+static hipError_t launch_one(const MdqDesc *d, int n, long long tiles, unsigned long long *prof,
+                             unsigned long long seed, int grid, hipStream_t s)
+{
+    hipLaunchKernelGGL((mdq_step_kernel<ST, GT, LOG2B, SR>), dim3(grid), dim3(256), 0, s,
+                       d, n, tiles, prof, seed);
+    return hipGetLastError();
+}
+
+template <int ST, int GT, bool SR>
+static hipError_t launch_b(int log2b, const MdqDesc *d, int n, long long tiles,
+                           unsigned long long *prof, unsigned long long seed, int grid, hipStream_t s)
+{
+    switch (log2b) {
+    case 0: return launch_one<ST, GT, 0, SR>(d, n, tiles, prof, seed, grid, s);
+    case 1: return launch_one<ST, GT, 1, SR>(d, n, tiles, prof, seed, grid, s);
+    case 2: return launch_one<ST, GT, 2, SR>(d, n, tiles, prof, seed, grid, s);
+    case 3: return launch_one<ST, GT, 3, SR>(d, n, tiles, prof, seed, grid, s);
+    case 4: return launch_one<ST, GT, 4, SR>(d, n, tiles, prof, seed, grid, s);
+    case 5: return launch_one<ST, GT, 5, SR>(d, n, tiles, prof, seed, grid, s);
+    case 6: return launch_one<ST, GT, 6, SR>(d, n, tiles, prof, seed, grid, s);
+    case 7: return launch_one<ST, GT, 7, SR>(d, n, tiles, prof, seed, grid, s);
+    case 8: return launch_one<ST, GT, 8, SR>(d, n, tiles, prof, seed, grid, s);
+    case 9: return launch_one<ST, GT, 9, SR>(d, n, tiles, prof, seed, grid, s);
+    case 10: return launch_one<ST, GT, 10, SR>(d, n, tiles, prof, seed, grid, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+template <int ST>
+static hipError_t launch_for(const MdqDesc *d, int n, long long tiles, int gt, int log2b, bool sr,
+                             unsigned long long *prof, unsigned long long seed, int grid, hipStream_t s)
+{
+    switch (gt) {
+    case GT_F32: return sr ? launch_b<ST, GT_F32, true>(log2b, d, n, tiles, prof, seed, grid, s)
+                           : launch_b<ST, GT_F32, false>(log2b, d, n, tiles, prof, seed, grid, s);
+    case GT_BF16: return sr ? launch_b<ST, GT_BF16, true>(log2b, d, n, tiles, prof, seed, grid, s)
+                            : launch_b<ST, GT_BF16, false>(log2b, d, n, tiles, prof, seed, grid, s);
+    case GT_F16: return sr ? launch_b<ST, GT_F16, true>(log2b, d, n, tiles, prof, seed, grid, s)
+                           : launch_b<ST, GT_F16, false>(log2b, d, n, tiles, prof, seed, grid, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace mdq

@@ -1,0 +1,502 @@
+// mdq_kernel.h -- the fused dequant -> AdamW -> requant step for gfx950.
+//
+// One launch walks every tensor of a (storage, grad dtype, block size,
+// rounding) class from a packed MdqDesc table.  Semantics per element follow
+// /root/reference/CUDA/stquant_kernel.cu:53-401 (see mdq_step_tile below for
+// the line-by-line map); the layout and schedule are this file's own:
+//
+// * A tile is 256 lanes x EPL elements (EPL = 8 for B >= 8).  A quant block
+//   of B elements is owned by LPB = B/EPL consecutive lanes of one wave (two
+//   waves for B = 1024); lane j of a block owns quads j, j+LPB, ... so every
+//   16-lane row of a wave reads one contiguous 256-byte span per 16-byte load.
+// * Block reductions (max|m|, max/min log v) run in registers, then across
+//   the LPB lanes with DPP row operations (quad_perm, row_half_mirror,
+//   row_mirror), ds_swizzle for 32 lanes, ds_bpermute for 64, and an LDS
+//   exchange between the two waves of a 1024-element block.
+// * Packed 4-bit v codes dequantise through a 16-entry exp table per block
+//   built in LDS (16 exp per block instead of one per element).
+// * Requant uses mdq_round_half_away (exact fp32) for code widths <= 16 bits
+//   and the reference's FP64 divide + round for wider codes.
+// * The parameter update uses v_sqrt_f32 / v_rcp_f32 (the tolerance on p is
+//   1e-6 relative; codes and scales are exact).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "mdq_desc.h"
+#include "mdq_math.h"
+
+namespace mdq {
+
+template <int LOG2B>
+struct Cfg {
+    static constexpr int B = 1 << LOG2B;
+    static constexpr int EPL = B >= 8 ? 8 : B;            // elements per lane
+    static constexpr int LPB = B / EPL;                    // lanes per quant block
+    static constexpr int QPL = EPL >= 4 ? EPL / 4 : 0;     // 4-element quads per lane
+    static constexpr int TB = LPB <= 64 ? 256 / LPB : 2;   // quant blocks per tile
+    static constexpr int BPW = LPB <= 64 ? 64 / LPB : 0;   // quant blocks per wave
+    static constexpr int TILE = 256 * EPL;                 // elements per tile
+    static_assert(TB * B == TILE, "tile must hold whole blocks");
+};
+
+// Offset inside the quant block of lane j's element e.
+template <int LOG2B>
+__device__ __forceinline__ int elem_off(int j, int e)
+{
+    using C = Cfg<LOG2B>;
+    if constexpr (C::QPL > 0) return 4 * (j + (e >> 2) * C::LPB) + (e & 3);
+    else return e;
+}
+
+// ---------------------------------------------------------------- grad loads
+template <int GT> struct GradIO;
+template <> struct GradIO<GT_F32> {
+    static __device__ __forceinline__ void load4(const void *g, int64_t i, float *o) {
+        float4 v = *reinterpret_cast<const float4 *>(static_cast<const float *>(g) + i);
+        o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+    }
+    static __device__ __forceinline__ float load1(const void *g, int64_t i) {
+        return static_cast<const float *>(g)[i];
+    }
+};
+template <> struct GradIO<GT_BF16> {
+    static __device__ __forceinline__ void load4(const void *g, int64_t i, float *o) {
+        uint2 v = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(g) + i);
+        o[0] = bits_f(v.x << 16); o[1] = bits_f(v.x & 0xffff0000u);
+        o[2] = bits_f(v.y << 16); o[3] = bits_f(v.y & 0xffff0000u);
+    }
+    static __device__ __forceinline__ float load1(const void *g, int64_t i) {
+        return bits_f((uint32_t)static_cast<const uint16_t *>(g)[i] << 16);
+    }
+};
+template <> struct GradIO<GT_F16> {
+    static __device__ __forceinline__ float h2f(uint32_t h) {
+        return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+    }
+    static __device__ __forceinline__ void load4(const void *g, int64_t i, float *o) {
+        uint2 v = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(g) + i);
+        o[0] = h2f(v.x & 0xffffu); o[1] = h2f(v.x >> 16);
+        o[2] = h2f(v.y & 0xffffu); o[3] = h2f(v.y >> 16);
+    }
+    static __device__ __forceinline__ float load1(const void *g, int64_t i) {
+        return h2f(static_cast<const uint16_t *>(g)[i]);
+    }
+};
+
+// ---------------------------------------------------------------- code I/O
+// mc: the m code as float, already minus 8 for packed nibbles (the value the
+// reference multiplies by scale_m); vc: the raw v code.
+template <int ST> struct CodeIO;
+template <> struct CodeIO<ST_P4> {
+    static __device__ __forceinline__ void load4(const MdqDesc &d, int64_t i, float *mc, uint32_t *vc) {
+        uint32_t w = *reinterpret_cast<const uint32_t *>(static_cast<const uint8_t *>(d.code_m) + i);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            uint32_t b = (w >> (8 * k)) & 0xffu;
+            mc[k] = (float)(b & 15u) - 8.0f;
+            vc[k] = b >> 4;
+        }
+    }
+    static __device__ __forceinline__ void load1(const MdqDesc &d, int64_t i, float &mc, uint32_t &vc) {
+        uint32_t b = static_cast<const uint8_t *>(d.code_m)[i];
+        mc = (float)(b & 15u) - 8.0f;
+        vc = b >> 4;
+    }
+    static __device__ __forceinline__ uint32_t pack(int32_t qm, uint32_t qv) {
+        return (qv << 4) | (uint32_t)(qm + 8);
+    }
+    static __device__ __forceinline__ void store4(const MdqDesc &d, int64_t i, const int32_t *qm, const uint32_t *qv) {
+        uint32_t w = pack(qm[0], qv[0]) | (pack(qm[1], qv[1]) << 8) |
+                     (pack(qm[2], qv[2]) << 16) | (pack(qm[3], qv[3]) << 24);
+        *reinterpret_cast<uint32_t *>(static_cast<uint8_t *>(d.code_m) + i) = w;
+    }
+    static __device__ __forceinline__ void store1(const MdqDesc &d, int64_t i, int32_t qm, uint32_t qv) {
+        static_cast<uint8_t *>(d.code_m)[i] = (uint8_t)pack(qm, qv);
+    }
+};
+template <> struct CodeIO<ST_S8> {
+    static __device__ __forceinline__ void load4(const MdqDesc &d, int64_t i, float *mc, uint32_t *vc) {
+        uint32_t wm = *reinterpret_cast<const uint32_t *>(static_cast<const int8_t *>(d.code_m) + i);
+        uint32_t wv = *reinterpret_cast<const uint32_t *>(static_cast<const uint8_t *>(d.code_v) + i);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            mc[k] = (float)(int8_t)(wm >> (8 * k));
+            vc[k] = (wv >> (8 * k)) & 0xffu;
+        }
+    }
+    static __device__ __forceinline__ void load1(const MdqDesc &d, int64_t i, float &mc, uint32_t &vc) {
+        mc = (float)static_cast<const int8_t *>(d.code_m)[i];
+        vc = static_cast<const uint8_t *>(d.code_v)[i];
+    }
+    static __device__ __forceinline__ void store4(const MdqDesc &d, int64_t i, const int32_t *qm, const uint32_t *qv) {
+        uint32_t wm = 0, wv = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            wm |= ((uint32_t)qm[k] & 0xffu) << (8 * k);
+            wv |= (qv[k] & 0xffu) << (8 * k);
+        }
+        *reinterpret_cast<uint32_t *>(static_cast<int8_t *>(d.code_m) + i) = wm;
+        *reinterpret_cast<uint32_t *>(static_cast<uint8_t *>(d.code_v) + i) = wv;
+    }
+    static __device__ __forceinline__ void store1(const MdqDesc &d, int64_t i, int32_t qm, uint32_t qv) {
+        static_cast<int8_t *>(d.code_m)[i] = (int8_t)qm;
+        static_cast<uint8_t *>(d.code_v)[i] = (uint8_t)qv;
+    }
+};
+template <> struct CodeIO<ST_S16> {
+    static __device__ __forceinline__ void load4(const MdqDesc &d, int64_t i, float *mc, uint32_t *vc) {
+        uint2 wm = *reinterpret_cast<const uint2 *>(static_cast<const int16_t *>(d.code_m) + i);
+        uint2 wv = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(d.code_v) + i);
+        mc[0] = (float)(int16_t)wm.x; mc[1] = (float)(int16_t)(wm.x >> 16);
+        mc[2] = (float)(int16_t)wm.y; mc[3] = (float)(int16_t)(wm.y >> 16);
+        vc[0] = wv.x & 0xffffu; vc[1] = wv.x >> 16; vc[2] = wv.y & 0xffffu; vc[3] = wv.y >> 16;
+    }
+    static __device__ __forceinline__ void load1(const MdqDesc &d, int64_t i, float &mc, uint32_t &vc) {
+        mc = (float)static_cast<const int16_t *>(d.code_m)[i];
+        vc = static_cast<const uint16_t *>(d.code_v)[i];
+    }
+    static __device__ __forceinline__ void store4(const MdqDesc &d, int64_t i, const int32_t *qm, const uint32_t *qv) {
+        uint2 wm, wv;
+        wm.x = ((uint32_t)qm[0] & 0xffffu) | ((uint32_t)qm[1] << 16);
+        wm.y = ((uint32_t)qm[2] & 0xffffu) | ((uint32_t)qm[3] << 16);
+        wv.x = (qv[0] & 0xffffu) | (qv[1] << 16);
+        wv.y = (qv[2] & 0xffffu) | (qv[3] << 16);
+        *reinterpret_cast<uint2 *>(static_cast<int16_t *>(d.code_m) + i) = wm;
+        *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(d.code_v) + i) = wv;
+    }
+    static __device__ __forceinline__ void store1(const MdqDesc &d, int64_t i, int32_t qm, uint32_t qv) {
+        static_cast<int16_t *>(d.code_m)[i] = (int16_t)qm;
+        static_cast<uint16_t *>(d.code_v)[i] = (uint16_t)qv;
+    }
+};
+template <> struct CodeIO<ST_S32> {
+    static __device__ __forceinline__ void load4(const MdqDesc &d, int64_t i, float *mc, uint32_t *vc) {
+        int4 wm = *reinterpret_cast<const int4 *>(static_cast<const int32_t *>(d.code_m) + i);
+        uint4 wv = *reinterpret_cast<const uint4 *>(static_cast<const uint32_t *>(d.code_v) + i);
+        mc[0] = (float)wm.x; mc[1] = (float)wm.y; mc[2] = (float)wm.z; mc[3] = (float)wm.w;
+        vc[0] = wv.x; vc[1] = wv.y; vc[2] = wv.z; vc[3] = wv.w;
+    }
+    static __device__ __forceinline__ void load1(const MdqDesc &d, int64_t i, float &mc, uint32_t &vc) {
+        mc = (float)static_cast<const int32_t *>(d.code_m)[i];
+        vc = static_cast<const uint32_t *>(d.code_v)[i];
+    }
+    static __device__ __forceinline__ void store4(const MdqDesc &d, int64_t i, const int32_t *qm, const uint32_t *qv) {
+        *reinterpret_cast<int4 *>(static_cast<int32_t *>(d.code_m) + i) = make_int4(qm[0], qm[1], qm[2], qm[3]);
+        *reinterpret_cast<uint4 *>(static_cast<uint32_t *>(d.code_v) + i) = make_uint4(qv[0], qv[1], qv[2], qv[3]);
+    }
+    static __device__ __forceinline__ void store1(const MdqDesc &d, int64_t i, int32_t qm, uint32_t qv) {
+        static_cast<int32_t *>(d.code_m)[i] = qm;
+        static_cast<uint32_t *>(d.code_v)[i] = qv;
+    }
+};
+
+// ------------------------------------------------------- cross-lane reduction
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x)
+{
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
+}
+
+template <bool IS_MAX>
+__device__ __forceinline__ float op_(float a, float b) { return IS_MAX ? fmaxf(a, b) : fminf(a, b); }
+
+// Reduce over aligned groups of LANES lanes (LANES <= 64); every lane of the
+// group receives the result.
+template <int LANES, bool IS_MAX>
+__device__ __forceinline__ float group_reduce(float x)
+{
+    if constexpr (LANES >= 2) x = op_<IS_MAX>(x, dpp_f<0xB1>(x));   // quad_perm [1,0,3,2]
+    if constexpr (LANES >= 4) x = op_<IS_MAX>(x, dpp_f<0x4E>(x));   // quad_perm [2,3,0,1]
+    if constexpr (LANES >= 8) x = op_<IS_MAX>(x, dpp_f<0x141>(x));  // row_half_mirror
+    if constexpr (LANES >= 16) x = op_<IS_MAX>(x, dpp_f<0x140>(x)); // row_mirror
+    if constexpr (LANES >= 32)                                      // lane ^ 16 within 32
+        x = op_<IS_MAX>(x, __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), 0x401F)));
+    if constexpr (LANES >= 64) x = op_<IS_MAX>(x, __shfl_xor(x, 32));
+    return x;
+}
+
+struct ProfAcc {
+    unsigned long long c[5];
+};
+
+// ---------------------------------------------------------------- one tile
+// FULL: every element of the tile lies inside the tensor and all pointers are
+// 16-byte aligned, so vector accesses are used; otherwise every access is
+// guarded by idx < numel.
+template <int ST, int GT, int LOG2B, bool SR, bool FULL>
+__device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int lane, int wave,
+                                              float *lut, float *xw, unsigned long long seed,
+                                              bool prof_on, ProfAcc &pa)
+{
+    using C = Cfg<LOG2B>;
+    constexpr int B = C::B, EPL = C::EPL, LPB = C::LPB;
+    constexpr bool USE_LUT = (ST == ST_P4) && B >= 32;
+
+    unsigned long long t0 = 0;
+    if (prof_on) t0 = clock64();
+
+    int bi, j;
+    if constexpr (LPB <= 64) { bi = wave * C::BPW + lane / LPB; j = lane % LPB; }
+    else { bi = wave >> 1; j = ((wave & 1) << 6) | lane; }
+    const int64_t n = d.numel;
+    const int64_t blk = tl * C::TB + bi;
+    const int64_t base = blk << LOG2B;
+    const bool blk_ok = FULL || base < n;
+
+    // old block scales (stquant_kernel.cu:67-69)
+    float sm = 0.0f, sv = 0.0f, vmin = 0.0f;
+    if (blk_ok) { sm = d.scale_m[blk]; sv = d.scale_v[blk]; vmin = d.v_min[blk]; }
+
+    float pv[EPL], gv[EPL], mc[EPL];
+    uint32_t vc[EPL];
+    bool ok[EPL];
+    if constexpr (FULL && C::QPL > 0) {
+#pragma unroll
+        for (int k = 0; k < C::QPL; ++k) {
+            const int64_t i = base + 4 * (j + k * LPB);
+            float4 p4 = *reinterpret_cast<const float4 *>(d.p + i);
+            pv[4 * k + 0] = p4.x; pv[4 * k + 1] = p4.y; pv[4 * k + 2] = p4.z; pv[4 * k + 3] = p4.w;
+            GradIO<GT>::load4(d.g, i, gv + 4 * k);
+            CodeIO<ST>::load4(d, i, mc + 4 * k, vc + 4 * k);
+        }
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) ok[e] = true;
+    } else {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+            const int64_t i = base + elem_off<LOG2B>(j, e);
+            ok[e] = FULL || i < n;
+            pv[e] = 0.0f; gv[e] = 0.0f; mc[e] = 0.0f; vc[e] = 0;
+            if (ok[e]) {
+                pv[e] = d.p[i];
+                gv[e] = GradIO<GT>::load1(d.g, i);
+                CodeIO<ST>::load1(d, i, mc[e], vc[e]);
+            }
+        }
+    }
+
+    // exp table of the 16 packed v codes of this block (stquant_kernel.cu:75)
+    if constexpr (USE_LUT) {
+        float *tab = lut + bi * 16;
+        if (blk_ok) {
+#pragma unroll
+            for (int r = 0; r < (16 + LPB - 1) / LPB; ++r) {
+                const int e = j + r * LPB;
+                if (e < 16) tab[e] = mdq_expf(fma_((float)e, sv, vmin));
+            }
+        }
+        if constexpr (LPB <= 64) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        } else {
+            __syncthreads();
+        }
+    }
+    if (prof_on) { unsigned long long t = clock64(); pa.c[0] += t - t0; t0 = t; }
+
+    // dequant + AdamW moments (stquant_kernel.cu:71-85); contraction fixed as
+    // one fma for the v exponent and one for each moment.
+    float m[EPL], v[EPL], lv[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+        const float m0 = mc[e] * sm;
+        float v0;
+        if constexpr (USE_LUT) v0 = lut[bi * 16 + vc[e]];
+        else v0 = mdq_expf(fma_((float)vc[e], sv, vmin));
+        const float g = gv[e];
+        m[e] = fma_(d.b1, m0, d.omb1 * g);
+        v[e] = fma_(d.b2, v0, (d.omb2 * g) * g);
+    }
+    if (prof_on) { unsigned long long t = clock64(); pa.c[1] += t - t0; t0 = t; }
+
+    // |m|, log(v + 1e-12) and the three block reductions (:92-97); lanes
+    // outside the tensor contribute 0 to all three.
+    float amax, lmax, lmin;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+        const float a = ok[e] ? fabsf(m[e]) : 0.0f;
+        const float l = ok[e] ? mdq_logf(v[e] + 1e-12f) : 0.0f;
+        lv[e] = l;
+        if (e == 0) { amax = a; lmax = l; lmin = l; }
+        else { amax = fmaxf(amax, a); lmax = fmaxf(lmax, l); lmin = fminf(lmin, l); }
+    }
+    if constexpr (LPB <= 64) {
+        amax = group_reduce<LPB, true>(amax);
+        lmax = group_reduce<LPB, true>(lmax);
+        lmin = group_reduce<LPB, false>(lmin);
+    } else {
+        amax = group_reduce<64, true>(amax);
+        lmax = group_reduce<64, true>(lmax);
+        lmin = group_reduce<64, false>(lmin);
+        if (lane == 0) { xw[wave * 3 + 0] = amax; xw[wave * 3 + 1] = lmax; xw[wave * 3 + 2] = lmin; }
+        __syncthreads();
+        const int o = (wave ^ 1) * 3;
+        amax = fmaxf(amax, xw[o + 0]);
+        lmax = fmaxf(lmax, xw[o + 1]);
+        lmin = fminf(lmin, xw[o + 2]);
+    }
+
+    // new scales (:101-106)
+    const float s_sm = (amax + 1e-12f) * d.inv_qm;            // == / 2^(bits-1), exact
+    const float s_sv = ((lmax - lmin) + 1e-12f) / d.qvf;      // IEEE division
+    const float s_vmin = lmin;
+    if (j == 0 && blk_ok) {
+        d.scale_m[blk] = s_sm;
+        d.scale_v[blk] = s_sv;
+        d.v_min[blk] = s_vmin;
+    }
+    if (prof_on) { unsigned long long t = clock64(); pa.c[2] += t - t0; t0 = t; }
+
+    // requant (:112-131)
+    const float dm = s_sm + 1e-12f, dv = s_sv + 1e-12f;
+    const float hdm = 0.5f * dm, hdv = 0.5f * dv;
+    int32_t qmi[EPL];
+    uint32_t qvi[EPL];
+    const bool wide = (ST == ST_S32) && d.bits > 16;          // uniform per tensor
+    if (!wide) {
+        float inv_dm, inv_dv;
+        if constexpr (SR) { inv_dm = 1.0f / dm; inv_dv = 1.0f / dv; }
+        else { inv_dm = __builtin_amdgcn_rcpf(dm); inv_dv = __builtin_amdgcn_rcpf(dv); }
+        float um[EPL], uv[EPL];
+        if constexpr (SR) {
+            // Philox4x32-10 per 4-element quad of the tensor: counter
+            // (quad index lo, hi, tensor id, step), key = seed; word i of the
+            // output serves element 4q+i (low half -> m, high half -> v).
+            if constexpr (C::QPL > 0) {
+#pragma unroll
+                for (int k = 0; k < C::QPL; ++k) {
+                    const uint64_t q = (uint64_t)((base >> 2) + j + k * LPB);
+                    U4 r = mdq_philox4x32_10(U4{(uint32_t)q, (uint32_t)(q >> 32), d.tensor_id, d.step},
+                                             (uint32_t)seed, (uint32_t)(seed >> 32));
+                    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        um[4 * k + i] = mdq_u16_uniform(w[i] & 0xffffu);
+                        uv[4 * k + i] = mdq_u16_uniform(w[i] >> 16);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) {
+                    const uint64_t idx = (uint64_t)(base + e);
+                    const uint64_t q = idx >> 2;
+                    U4 r = mdq_philox4x32_10(U4{(uint32_t)q, (uint32_t)(q >> 32), d.tensor_id, d.step},
+                                             (uint32_t)seed, (uint32_t)(seed >> 32));
+                    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
+                    const uint32_t ww = w[idx & 3];
+                    um[e] = mdq_u16_uniform(ww & 0xffffu);
+                    uv[e] = mdq_u16_uniform(ww >> 16);
+                }
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+            float qmf, qvf;
+            const float u = lv[e] - s_vmin;
+            if constexpr (SR) {
+                qmf = floor_(fma_(m[e], inv_dm, um[e]));
+                qvf = floor_(fma_(u, inv_dv, uv[e]));
+            } else {
+                const float K = mdq_round_half_away(fabsf(m[e]), dm, inv_dm, hdm);
+                qmf = m[e] < 0.0f ? -K : K;
+                qvf = mdq_round_half_away(u, dv, inv_dv, hdv);
+            }
+            qmf = fminf(fmaxf(qmf, -d.qm), d.qm - 1.0f);
+            qvf = fminf(fmaxf(qvf, 0.0f), d.qv);
+            qmi[e] = (int32_t)qmf;
+            qvi[e] = (uint32_t)(int32_t)qvf;
+        }
+    } else {
+        // 17..32-bit codes: the reference's FP64 path verbatim.
+        const double qlm = (double)d.qm;                        // 2^(bits-1), exact
+        const double qlv = __builtin_ldexp(1.0, (int)d.bits) - 1.0;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+            double qm_ = __builtin_round((double)m[e] / (double)dm);
+            qm_ = qm_ < -qlm ? -qlm : qm_;
+            qm_ = qm_ > qlm - 1.0 ? qlm - 1.0 : qm_;
+            double qv_ = __builtin_round((double)(lv[e] - s_vmin) / (double)dv);
+            qv_ = qv_ < 0.0 ? 0.0 : qv_;
+            qv_ = qv_ > qlv ? qlv : qv_;
+            qmi[e] = (int32_t)qm_;
+            qvi[e] = (uint32_t)qv_;
+        }
+    }
+    if (prof_on) { unsigned long long t = clock64(); pa.c[3] += t - t0; t0 = t; }
+
+    // parameter update with the unquantised m, v (:135-144)
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+        const float den = fma_(__builtin_amdgcn_sqrtf(v[e]), d.inv_sqrt_bc2, d.eps);
+        const float upd = m[e] * __builtin_amdgcn_rcpf(den);
+        pv[e] = fma_(-d.step_size, upd, pv[e] * d.decay);
+    }
+
+    if constexpr (FULL && C::QPL > 0) {
+#pragma unroll
+        for (int k = 0; k < C::QPL; ++k) {
+            const int64_t i = base + 4 * (j + k * LPB);
+            CodeIO<ST>::store4(d, i, qmi + 4 * k, qvi + 4 * k);
+            *reinterpret_cast<float4 *>(d.p + i) =
+                make_float4(pv[4 * k + 0], pv[4 * k + 1], pv[4 * k + 2], pv[4 * k + 3]);
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+            if (ok[e]) {
+                const int64_t i = base + elem_off<LOG2B>(j, e);
+                CodeIO<ST>::store1(d, i, qmi[e], qvi[e]);
+                d.p[i] = pv[e];
+            }
+        }
+    }
+    if (prof_on) { unsigned long long t = clock64(); pa.c[4] += t - t0; }
+}
+
+template <int ST, int GT, int LOG2B, bool SR>
+__global__ __launch_bounds__(256) void mdq_step_kernel(const MdqDesc *__restrict__ descs, int n_desc,
+                                                       long long total_tiles,
+                                                       unsigned long long *__restrict__ prof,
+                                                       unsigned long long seed)
+{
+    using C = Cfg<LOG2B>;
+    constexpr bool USE_LUT = (ST == ST_P4) && C::B >= 32;
+    __shared__ float lut_s[2][USE_LUT ? C::TB * 16 : 1];
+    __shared__ float xw_s[2][12];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+
+    long long tile = blockIdx.x;
+    if (tile >= total_tiles) return;
+    // first tensor: largest t with tile_begin <= tile
+    int lo = 0, hi = n_desc - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (descs[mid].tile_begin <= tile) lo = mid;
+        else hi = mid - 1;
+    }
+    int ti = __builtin_amdgcn_readfirstlane(lo);
+    ProfAcc pa = {{0, 0, 0, 0, 0}};
+    const bool prof_on = prof != nullptr;
+    int parity = 0;
+    for (; tile < total_tiles; tile += gridDim.x) {
+        while (descs[ti].tile_end <= tile) ++ti;
+        const MdqDesc &d = descs[ti];
+        const long long tl = tile - d.tile_begin;
+        const bool full = (d.flags & DF_ALIGNED) && (tl + 1) * C::TILE <= d.numel;
+        float *lut = lut_s[parity];
+        float *xw = xw_s[parity];
+        if (full) mdq_step_tile<ST, GT, LOG2B, SR, true>(d, tl, lane, wave, lut, xw, seed, prof_on, pa);
+        else mdq_step_tile<ST, GT, LOG2B, SR, false>(d, tl, lane, wave, lut, xw, seed, prof_on, pa);
+        parity ^= 1;
+    }
+    if (prof_on) {
+        if (lane == 0) {
+#pragma unroll
+            for (int s = 0; s < 5; ++s) atomicAdd(prof + s, pa.c[s]);
+        }
+    }
+}
+
+}  // namespace mdq

@@ -1,0 +1,19 @@
+// mdq_launch.h -- host entry points of the kernel instances (one per storage
+// class) and of the math self-check kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "mdq_desc.h"
+
+namespace mdq {
+
+hipError_t launch_p4(const MdqDesc *, int, long long, int, int, bool, unsigned long long *, unsigned long long, int, hipStream_t);
+hipError_t launch_s8(const MdqDesc *, int, long long, int, int, bool, unsigned long long *, unsigned long long, int, hipStream_t);
+hipError_t launch_s16(const MdqDesc *, int, long long, int, int, bool, unsigned long long *, unsigned long long, int, hipStream_t);
+hipError_t launch_s32(const MdqDesc *, int, long long, int, int, bool, unsigned long long *, unsigned long long, int, hipStream_t);
+
+hipError_t launch_math(int which, const float *x, float *y, long long n, hipStream_t s);
+hipError_t launch_math_digests(int which, unsigned first, unsigned count, unsigned chunk,
+                               unsigned long long *dig, hipStream_t s);
+
+}  // namespace mdq

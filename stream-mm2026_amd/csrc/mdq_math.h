@@ -1,0 +1,139 @@
+// mdq_math.h -- fp32 math of the fused MDQ AdamW step, compiled for both the
+// gfx950 device pass and the host pass of hipcc.
+//
+// The device kernels use these functions; the host copies are exported by the
+// C-ABI library (stq_host_*) so that the same source can be checked on a CPU.
+//
+// * mdq_expf / mdq_logf: faithful (< 1 ulp) replacements for the CUDA expf /
+//   logf calls of /root/reference/CUDA/stquant_kernel.cu:75,93.  Cody-Waite
+//   exp with a degree-5 minimax polynomial, and log over f in [2/3, 4/3) with
+//   a degree-8 minimax polynomial; coefficients are fp32 bit patterns.  Only
+//   IEEE fma/mul/add, rint, ldexp and integer bit operations are used, in a
+//   fixed order, and the library is built with -ffp-contract=off, so every
+//   caller gets the same bits on any IEEE-conforming target.
+// * mdq_round_half_away: round(u / d) for u >= 0 with ties away from zero,
+//   exactly as round((double)u / (double)d) (stquant_kernel.cu:113,123)
+//   evaluates for quotients below 2^17, using fp32 fma residuals only.
+// * mdq_philox4x32_10: Philox4x32-10 (Salmon et al., SC'11).
+#pragma once
+#include <stdint.h>
+
+#if defined(__HIPCC__)
+#define MDQ_HD __host__ __device__ __forceinline__
+#else
+#define MDQ_HD static inline
+#endif
+
+namespace mdq {
+
+MDQ_HD float bits_f(uint32_t u) { return __builtin_bit_cast(float, u); }
+MDQ_HD uint32_t f_bits(float f) { return __builtin_bit_cast(uint32_t, f); }
+
+#if defined(__HIP_DEVICE_COMPILE__)
+MDQ_HD float fma_(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
+MDQ_HD float rint_(float a) { return __builtin_rintf(a); }
+MDQ_HD float floor_(float a) { return __builtin_floorf(a); }
+MDQ_HD float ldexp_(float a, int e) { return __builtin_amdgcn_ldexpf(a, e); }
+#else
+MDQ_HD float fma_(float a, float b, float c) { return __builtin_fmaf(a, b, c); }
+MDQ_HD float rint_(float a) { return __builtin_rintf(a); }
+MDQ_HD float floor_(float a) { return __builtin_floorf(a); }
+MDQ_HD float ldexp_(float a, int e) { return __builtin_ldexpf(a, e); }
+#endif
+
+// e^x.  NaN -> NaN, x > 89 -> +inf, x < -104 -> 0; in between the result is
+// 2^k * (1 + (r + r^2 E(r))) with a single rounding in the final scale.
+MDQ_HD float mdq_expf(float x)
+{
+    const float log2e = bits_f(0x3fb8aa3bu);
+    const float ln2_hi = bits_f(0x3f317218u);
+    const float ln2_lo = bits_f(0xb102e308u);
+    // Clamp first so the integer conversion below is always in range; the
+    // special results are selected at the end.
+    float xc = x < -104.0f ? -104.0f : x;
+    xc = xc > 89.0f ? 89.0f : xc;
+    xc = (x == x) ? xc : 0.0f;
+    float kf = rint_(xc * log2e);
+    float r = fma_(-kf, ln2_hi, xc);
+    r = fma_(-kf, ln2_lo, r);
+    float q = bits_f(0x3950bf17u);
+    q = fma_(q, r, bits_f(0x3ab6a1a3u));
+    q = fma_(q, r, bits_f(0x3c088856u));
+    q = fma_(q, r, bits_f(0x3d2aaa74u));
+    q = fma_(q, r, bits_f(0x3e2aaaabu));
+    q = fma_(q, r, bits_f(0x3f000000u));
+    float r2 = r * r;
+    float t = fma_(r2, q, r);
+    float e = 1.0f + t;
+    float res = ldexp_(e, (int)kf);
+    res = x > 89.0f ? bits_f(0x7f800000u) : res;
+    res = x < -104.0f ? 0.0f : res;
+    return (x == x) ? res : x;
+}
+
+// log(x) for x a positive normal float, +inf or NaN (returned unchanged).
+// The kernel only ever evaluates log(v + 1e-12f) with v >= 0, a positive
+// normal; zero, denormal and negative inputs are outside this function's
+// domain.
+MDQ_HD float mdq_logf(float x)
+{
+    uint32_t ix = f_bits(x);
+    int32_t t = (int32_t)(ix - 0x3f2aaaabu);
+    int32_t k = t >> 23;
+    float f = bits_f(((uint32_t)t & 0x007fffffu) + 0x3f2aaaabu);
+    float r = f - 1.0f;
+    float kf = (float)k;
+    float p = bits_f(0xbe05ac99u);
+    p = fma_(p, r, bits_f(0x3e0cde1du));
+    p = fma_(p, r, bits_f(0xbdf8cd34u));
+    p = fma_(p, r, bits_f(0x3e0fea42u));
+    p = fma_(p, r, bits_f(0xbe2ad591u));
+    p = fma_(p, r, bits_f(0x3e4cdfffu));
+    p = fma_(p, r, bits_f(0xbe7fff4au));
+    p = fma_(p, r, bits_f(0x3eaaaa96u));
+    p = fma_(p, r, bits_f(0xbf000000u));
+    float r2 = r * r;
+    float lo = fma_(kf, bits_f(0x35bfbe8eu), r2 * p);
+    float res = fma_(kf, bits_f(0x3f317200u), r + lo);
+    return ix >= 0x7f800000u ? x : res;
+}
+
+// K = floor(u/d + 1/2) for u >= 0 and d a positive normal float, i.e.
+// round-half-away(u/d).  Exact whenever the candidate k0 = floor(u*inv_d + .5)
+// is within one of u/d, which holds for u/d < 2^17 and inv_d within 2 ulp of
+// 1/d.  Then R = u - k0*d is exactly representable (u >= d/2 puts u and k0*d
+// on a common 2^(E_d-24) grid, |R| <= d), and the decisions R >= d/2 and
+// R < -d/2 are exact; u < d/2 always rounds to 0.  hd must be d/2 exactly.
+MDQ_HD float mdq_round_half_away(float u, float d, float inv_d, float hd)
+{
+    float k0 = floor_(fma_(u, inv_d, 0.5f));
+    float R = fma_(-k0, d, u);
+    float K = k0;
+    K = (R >= hd) ? K + 1.0f : K;
+    K = (R < -hd) ? K - 1.0f : K;
+    return (u < hd) ? 0.0f : K;
+}
+
+struct U4 { uint32_t x, y, z, w; };
+
+MDQ_HD U4 mdq_philox4x32_10(U4 c, uint32_t k0, uint32_t k1)
+{
+#pragma unroll
+    for (int r = 0; r < 10; ++r) {
+        if (r) { k0 += 0x9E3779B9u; k1 += 0xBB67AE85u; }
+        uint64_t p0 = (uint64_t)0xD2511F53u * c.x;
+        uint64_t p1 = (uint64_t)0xCD9E8D57u * c.z;
+        U4 n;
+        n.x = (uint32_t)(p1 >> 32) ^ c.y ^ k0;
+        n.y = (uint32_t)p1;
+        n.z = (uint32_t)(p0 >> 32) ^ c.w ^ k1;
+        n.w = (uint32_t)p0;
+        c = n;
+    }
+    return c;
+}
+
+// Uniforms on the centred 2^-16 grid: (k + 1/2) / 65536, k in [0, 65535].
+MDQ_HD float mdq_u16_uniform(uint32_t k16) { return ((float)k16 + 0.5f) * (1.0f / 65536.0f); }
+
+}  // namespace mdq

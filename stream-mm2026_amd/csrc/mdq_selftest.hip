@@ -1,0 +1,70 @@
+// Device-side evaluation of the step's fp32 math (mdq_math.h) so it can be
+// compared bit for bit with a CPU implementation.
+#include <hip/hip_runtime.h>
+
+#include "mdq_launch.h"
+#include "mdq_math.h"
+
+namespace mdq {
+
+__device__ __forceinline__ float eval_math(int which, float x)
+{
+    return which == 0 ? mdq_expf(x) : mdq_logf(x);
+}
+
+__global__ __launch_bounds__(256) void math_kernel(int which, const float *__restrict__ x,
+                                                   float *__restrict__ y, long long n)
+{
+    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (long long)gridDim.x * blockDim.x)
+        y[i] = eval_math(which, x[i]);
+}
+
+__device__ __forceinline__ unsigned long long mix64(unsigned long long z)
+{
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+}
+
+// Each thread sums 64 consecutive bit patterns (chunk is a multiple of 64, so
+// a run never straddles two chunks) and adds the sum to its chunk's digest.
+__global__ __launch_bounds__(256) void math_digest_kernel(int which, unsigned first, unsigned count,
+                                                          unsigned chunk,
+                                                          unsigned long long *__restrict__ dig)
+{
+    const unsigned long long runs = ((unsigned long long)count + 63) / 64;
+    for (unsigned long long r = (unsigned long long)blockIdx.x * blockDim.x + threadIdx.x; r < runs;
+         r += (unsigned long long)gridDim.x * blockDim.x) {
+        const unsigned off0 = (unsigned)(r * 64);
+        unsigned long long acc = 0;
+        for (unsigned k = 0; k < 64 && off0 + k < count; ++k) {
+            const unsigned b = first + off0 + k;
+            const float y = eval_math(which, bits_f(b));
+            acc += mix64(((unsigned long long)b << 32) | f_bits(y));
+        }
+        atomicAdd(dig + off0 / chunk, acc);
+    }
+}
+
+hipError_t launch_math(int which, const float *x, float *y, long long n, hipStream_t s)
+{
+    if (n <= 0) return hipSuccess;
+    long long blocks = (n + 255) / 256;
+    int grid = (int)(blocks < 65536 ? blocks : 65536);
+    hipLaunchKernelGGL(math_kernel, dim3(grid), dim3(256), 0, s, which, x, y, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_math_digests(int which, unsigned first, unsigned count, unsigned chunk,
+                               unsigned long long *dig, hipStream_t s)
+{
+    if (count == 0) return hipSuccess;
+    unsigned long long runs = ((unsigned long long)count + 63) / 64;
+    unsigned long long blocks = (runs + 255) / 256;
+    int grid = (int)(blocks < 65536 ? blocks : 65536);
+    hipLaunchKernelGGL(math_digest_kernel, dim3(grid), dim3(256), 0, s, which, first, count, chunk, dig);
+    return hipGetLastError();
+}
+
+}  // namespace mdq

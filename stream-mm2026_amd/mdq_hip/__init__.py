@@ -1,0 +1,242 @@
+"""MI355X-native fused dequant -> AdamW -> requant step (MDQ / STREAM optimizer).
+
+Host side of the C-ABI library ``libstquant_hip.so``.  Torch tensors are used
+only for device memory and streams; every call goes through the C ABI declared
+in ``include/stquant_hip.h`` and runs hand-written HIP kernels for gfx950.
+There is no CPU or eager-PyTorch fallback: a missing library raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import Optional, Sequence
+
+import torch
+
+from . import _capi
+from ._capi import ROUND_NEAREST, ROUND_STOCHASTIC, StqTensor, check, dtype_code, lib
+
+__all__ = [
+    "ROUND_NEAREST", "ROUND_STOCHASTIC", "TensorState", "MultiTensorPlan", "fused_step",
+    "multi_tensor_step",
+    "device_math", "device_math_digests", "host_math", "host_round_half_away", "host_philox",
+    "lib", "rounding_code",
+]
+
+
+def rounding_code(rounding) -> int:
+    if rounding in (ROUND_NEAREST, "nearest", None):
+        return ROUND_NEAREST
+    if rounding in (ROUND_STOCHASTIC, "stochastic"):
+        return ROUND_STOCHASTIC
+    raise ValueError(f"rounding must be 'nearest' or 'stochastic', got {rounding!r}")
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None or t.numel() == 0 else t.data_ptr()
+
+
+def _check_dense(name: str, t: torch.Tensor) -> None:
+    if not t.is_contiguous():
+        raise RuntimeError(f"{name} must be contiguous")
+
+
+def _profile_args(profile_cycles: Optional[torch.Tensor]):
+    # stquant_kernel.cu:403-412: undefined or empty -> off; else CUDA int64 with >= 5 slots.
+    if profile_cycles is None or profile_cycles.numel() == 0:
+        return None, 0
+    if not profile_cycles.is_cuda or profile_cycles.dtype != torch.int64:
+        raise RuntimeError("profile_cycles must be CUDA int64 tensor")
+    if profile_cycles.numel() < 5:
+        raise RuntimeError("profile_cycles needs >= 5 elements")
+    return profile_cycles.data_ptr(), profile_cycles.numel()
+
+
+def fused_step(p, grad, exp_avg, exp_avg_sq, scale_m, scale_v, v_min,
+               beta1, beta2, lr, weight_decay, eps, step, bits, block_size,
+               profile_cycles=None, *, rounding=ROUND_NEAREST, seed=0, tensor_id=0) -> None:
+    """One fused step on one tensor (the reference's ``fused_mdq_adamw``).
+
+    Checks and messages follow /root/reference/CUDA/stquant_kernel.cu:420-464.
+    """
+    if not (p.is_cuda and grad.is_cuda):
+        raise RuntimeError("p/grad must be CUDA")
+    if not exp_avg.is_cuda:
+        raise RuntimeError("exp_avg must be CUDA")
+    if p.dtype != torch.float32:
+        raise RuntimeError(f"expected scalar type Float but found {p.dtype}")
+    for name, t in (("scale_m", scale_m), ("scale_v", scale_v), ("v_min", v_min)):
+        if t.dtype != torch.float32:
+            raise RuntimeError(f"{name}: expected scalar type Float but found {t.dtype}")
+        if not t.is_cuda:
+            raise RuntimeError(f"{name} must be CUDA")
+        _check_dense(name, t)
+    for name, t in (("p", p), ("grad", grad), ("exp_avg", exp_avg), ("exp_avg_sq", exp_avg_sq)):
+        _check_dense(name, t)
+    if exp_avg_sq.numel() and not exp_avg_sq.is_cuda:
+        raise RuntimeError("exp_avg_sq must be CUDA")
+    prof_ptr, prof_n = _profile_args(profile_cycles)
+    L = lib()
+    with torch.cuda.device(p.device):
+        rc = L.stq_fused_mdq_adamw(
+            _ptr(p), _ptr(grad), dtype_code(grad.dtype), grad.numel(), p.numel(),
+            _ptr(exp_avg), dtype_code(exp_avg.dtype), exp_avg.numel(),
+            _ptr(exp_avg_sq), dtype_code(exp_avg_sq.dtype), exp_avg_sq.numel(),
+            _ptr(scale_m), scale_m.numel(), _ptr(scale_v), scale_v.numel(),
+            _ptr(v_min), v_min.numel(),
+            float(beta1), float(beta2), float(lr), float(weight_decay), float(eps),
+            int(step), int(bits), int(block_size),
+            prof_ptr, prof_n,
+            rounding_code(rounding), int(seed) & 0xFFFFFFFFFFFFFFFF, int(tensor_id) & 0xFFFFFFFF,
+            _capi.stream_handle(p.device))
+    check(rc)
+
+
+@dataclass
+class TensorState:
+    """One tensor of a multi-tensor step (state tensors as the optimizer keeps them)."""
+
+    p: torch.Tensor
+    grad: torch.Tensor
+    exp_avg: torch.Tensor
+    exp_avg_sq: torch.Tensor
+    scale_m: torch.Tensor
+    scale_v: torch.Tensor
+    v_min: torch.Tensor
+    step: int
+    bits: int
+    lr: float
+    beta1: float
+    beta2: float
+    eps: float
+    weight_decay: float
+    tensor_id: int = 0
+
+
+class MultiTensorPlan:
+    """A packed ``stq_tensor`` array for a fixed set of tensors.
+
+    Building the array costs a few microseconds per tensor; a plan is built
+    once and re-run, with only the per-tensor step (and optionally the grad
+    pointers) refreshed per call.  The tensors must stay alive and keep their
+    storage while the plan is used.
+    """
+
+    def __init__(self, entries: Sequence[TensorState], block_size: int, *,
+                 rounding=ROUND_NEAREST, seed: int = 0):
+        self.n = len(entries)
+        self.block_size = int(block_size)
+        self.rounding = rounding_code(rounding)
+        self.seed = int(seed) & 0xFFFFFFFFFFFFFFFF
+        self.entries = list(entries)
+        self.arr, self.codes = _pack_entries(self.entries)
+        self.device = self.entries[0].p.device if self.entries else None
+
+    def set_steps(self, steps) -> None:
+        if isinstance(steps, int):
+            for i in range(self.n):
+                self.arr[i].step = steps
+        else:
+            for i, s in enumerate(steps):
+                self.arr[i].step = int(s)
+
+    def run(self, profile_cycles: Optional[torch.Tensor] = None) -> None:
+        if self.n == 0:
+            return
+        prof_ptr, prof_n = _profile_args(profile_cycles)
+        gdt, eadt, easqdt = self.codes
+        with torch.cuda.device(self.device):
+            rc = lib().stq_multi_tensor_mdq_adamw(
+                self.arr, self.n, gdt, eadt, easqdt, self.block_size, self.rounding, self.seed,
+                prof_ptr, prof_n, _capi.stream_handle(self.device))
+        check(rc)
+
+
+def _pack_entries(entries: Sequence[TensorState]):
+    n = len(entries)
+    arr = (StqTensor * max(n, 1))()
+    if n == 0:
+        return arr, (0, 0, 0)
+    e0 = entries[0]
+    dev = e0.p.device
+    gdt, eadt, easqdt = e0.grad.dtype, e0.exp_avg.dtype, e0.exp_avg_sq.dtype
+    arr = (StqTensor * n)()
+    for i, e in enumerate(entries):
+        if e.p.device != dev or e.grad.device != dev:
+            raise RuntimeError("multi_tensor_step: all tensors must be on one device")
+        if e.grad.dtype != gdt or e.exp_avg.dtype != eadt or e.exp_avg_sq.dtype != easqdt:
+            raise RuntimeError("multi_tensor_step: grad and code dtypes must match across tensors")
+        if e.p.dtype != torch.float32:
+            raise RuntimeError(f"expected scalar type Float but found {e.p.dtype}")
+        for name, t in (("p", e.p), ("grad", e.grad), ("exp_avg", e.exp_avg),
+                        ("exp_avg_sq", e.exp_avg_sq), ("scale_m", e.scale_m),
+                        ("scale_v", e.scale_v), ("v_min", e.v_min)):
+            if not t.is_contiguous():
+                raise RuntimeError(f"{name} must be contiguous")
+        s = arr[i]
+        s.p = e.p.data_ptr(); s.grad = e.grad.data_ptr()
+        s.exp_avg = e.exp_avg.data_ptr()
+        s.exp_avg_sq = e.exp_avg_sq.data_ptr() if e.exp_avg_sq.numel() else None
+        s.scale_m = e.scale_m.data_ptr(); s.scale_v = e.scale_v.data_ptr(); s.v_min = e.v_min.data_ptr()
+        s.numel = e.p.numel(); s.grad_numel = e.grad.numel()
+        s.exp_avg_numel = e.exp_avg.numel(); s.exp_avg_sq_numel = e.exp_avg_sq.numel()
+        s.scale_m_numel = e.scale_m.numel(); s.scale_v_numel = e.scale_v.numel()
+        s.v_min_numel = e.v_min.numel()
+        s.beta1 = e.beta1; s.beta2 = e.beta2; s.lr = e.lr; s.weight_decay = e.weight_decay; s.eps = e.eps
+        s.step = int(e.step); s.bits = int(e.bits); s.tensor_id = int(e.tensor_id) & 0xFFFFFFFF
+    return arr, (dtype_code(gdt), dtype_code(eadt), dtype_code(easqdt))
+
+
+def multi_tensor_step(entries: Sequence[TensorState], block_size: int, *,
+                      rounding=ROUND_NEAREST, seed: int = 0,
+                      profile_cycles: Optional[torch.Tensor] = None) -> None:
+    """One launch over all ``entries`` (same device, code storage, grad dtype)."""
+    if len(entries) == 0:
+        return
+    MultiTensorPlan(entries, block_size, rounding=rounding, seed=seed).run(profile_cycles)
+
+
+def device_math(which: str, x: torch.Tensor) -> torch.Tensor:
+    """Device e^x (``which='exp'``) or log x (``'log'``) with the kernels' own fp32 code."""
+    assert x.is_cuda and x.dtype == torch.float32 and x.is_contiguous()
+    y = torch.empty_like(x)
+    with torch.cuda.device(x.device):
+        check(lib().stq_device_math(0 if which == "exp" else 1, _ptr(x), _ptr(y), x.numel(),
+                                    _capi.stream_handle(x.device)))
+    return y
+
+
+def device_math_digests(which: str, first: int, count: int, chunk: int, device=None) -> torch.Tensor:
+    device = torch.device(device or "cuda")
+    nchunks = (count + chunk - 1) // chunk
+    dig = torch.zeros(nchunks, dtype=torch.int64, device=device)
+    with torch.cuda.device(device):
+        check(lib().stq_device_math_digests(0 if which == "exp" else 1, first, count, chunk,
+                                            dig.data_ptr(), _capi.stream_handle(device)))
+    return dig
+
+
+def host_math(which: str, x) -> "numpy.ndarray":  # noqa: F821
+    import numpy as np
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    lib().stq_host_math(0 if which == "exp" else 1, x.ctypes.data, y.ctypes.data, x.size)
+    return y
+
+
+def host_round_half_away(u, d, inv_ulps: int = 0):
+    import numpy as np
+    u = np.ascontiguousarray(u, dtype=np.float32)
+    d = np.ascontiguousarray(d, dtype=np.float32)
+    out = np.empty_like(u)
+    lib().stq_host_round_half_away(u.ctypes.data, d.ctypes.data, out.ctypes.data, u.size, int(inv_ulps))
+    return out
+
+
+def host_philox(ctr, key):
+    import numpy as np
+    c = np.ascontiguousarray(np.asarray(ctr, dtype=np.uint32).reshape(4))
+    k = np.ascontiguousarray(np.asarray(key, dtype=np.uint32).reshape(2))
+    out = np.zeros(4, dtype=np.uint32)
+    lib().stq_host_philox4x32_10(c.ctypes.data, k.ctypes.data, out.ctypes.data)
+    return out

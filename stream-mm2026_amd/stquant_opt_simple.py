@@ -1,0 +1,604 @@
+"""MDQAdamWSimple -- drop-in for /root/reference/CUDA/stquant_opt_simple.py on MI355X.
+
+Same constructor, param groups, ``step()``, state layout (per param: ``step``,
+``exp_avg`` / ``exp_avg_sq`` integer codes -- packed nibbles in ``exp_avg`` and an
+empty ``exp_avg_sq`` at 4 bits --, ``scale_m``, ``scale_v``, ``v_min`` per quant
+block, ``current_bit``, ``last_score``), ``state_dict`` extras, bit-distribution
+getters and timing keys as the reference.
+
+What differs is underneath: instead of one kernel launch per tensor bracketed by
+two device synchronisations (:242-265), ``step()`` aligns the code storage of
+every tensor exactly as the reference does (:140-210), then runs ONE
+multi-tensor HIP launch per storage class through the C ABI of
+``libstquant_hip.so`` (``mdq_hip.multi_tensor_step``).  Results per element are
+those of the reference kernel (:246-263 -> stquant_kernel.cu).
+
+New optional param-group keys (defaults keep the reference behaviour):
+``bits`` (fixed code width 4/8/16/32 instead of the score-based choice),
+``rounding`` ('nearest' or 'stochastic') and ``seed`` (stochastic stream).
+``sync_timing=False`` skips the two device synchronisations that fill the
+timing dict.
+"""
+from __future__ import annotations
+
+import math
+import time
+from collections import OrderedDict
+
+import torch
+import torch.distributed as dist
+from torch.optim import Optimizer
+
+import mdq_hip
+
+
+class MDQAdamWSimple(Optimizer):
+    def __init__(
+        self,
+        params,
+        lr=1e-3,
+        betas=(0.9, 0.999),
+        eps=1e-8,
+        weight_decay=0.01,
+        alpha=0.9,
+        layer_count=24,
+        batch_size=32,
+        update_freq=20,
+        block_size=256,
+        bits=None,
+        rounding="nearest",
+        seed=0,
+        sync_timing=True,
+    ):
+        # stquant_opt_simple.py:33-44
+        tau_adaptive = 300 * math.log(layer_count) * math.sqrt(batch_size)
+        if bits is not None and int(bits) not in (4, 8, 16, 32):
+            raise ValueError(f"bits must be one of 4, 8, 16, 32 or None, got {bits}")
+        mdq_hip.rounding_code(rounding)
+        defaults = dict(
+            lr=lr,
+            betas=betas,
+            eps=eps,
+            weight_decay=weight_decay,
+            alpha=alpha,
+            tau=tau_adaptive,
+            update_freq=update_freq,
+            block_size=block_size,
+            bits=bits,
+            rounding=rounding,
+            seed=seed,
+        )
+        super().__init__(params, defaults)
+
+        self.n_ema = None
+        self.r_ema = None
+        self.v_global_ema = None
+        self.total_steps = 0
+        self.last_step_timings = {}
+        self.sync_timing = sync_timing
+        self._kernel_profile_buf = None
+        self._kernel_profile_device = None
+
+    _KERNEL_PROF_SLOTS = 5
+
+    # ------------------------------------------------------------------
+    # kernel phase profile (stquant_opt_simple.py:56-83)
+    # ------------------------------------------------------------------
+    def _kernel_profile_buf_for(self, device):
+        if self._kernel_profile_buf is None or self._kernel_profile_device != device:
+            self._kernel_profile_buf = torch.zeros(self._KERNEL_PROF_SLOTS, dtype=torch.int64, device=device)
+            self._kernel_profile_device = device
+        return self._kernel_profile_buf
+
+    def _reset_kernel_profile(self, device):
+        self._kernel_profile_buf_for(device).zero_()
+
+    def _read_kernel_profile_cycles(self, device):
+        buf = self._kernel_profile_buf_for(device)
+        return buf.double().cpu().tolist()
+
+    def _kernel_phases_ms_from_wall(self, device, kernel_wall_ms):
+        if kernel_wall_ms <= 0:
+            return [0.0] * self._KERNEL_PROF_SLOTS
+        cycles = self._read_kernel_profile_cycles(device)
+        total = sum(cycles)
+        if total <= 0:
+            return [0.0] * self._KERNEL_PROF_SLOTS
+        return [kernel_wall_ms * (c / total) for c in cycles]
+
+    @staticmethod
+    def _sync_device(device):
+        if device.type == "cuda":
+            torch.cuda.synchronize(device)
+
+    # ------------------------------------------------------------------
+    # grad stats and bit choice (stquant_opt_simple.py:93-109)
+    # ------------------------------------------------------------------
+    @staticmethod
+    def _compute_grad_stats(grad: torch.Tensor) -> torch.Tensor:
+        n_l = torch.sqrt(torch.mean(grad * grad))
+        r_l = torch.std(grad) / (grad.abs().mean() + 1e-12)
+        v_l = torch.mean(grad * grad)
+        return torch.stack([n_l, r_l, v_l])
+
+    @staticmethod
+    def _score_to_bits(score) -> int:
+        s = float(score.item()) if torch.is_tensor(score) and score.numel() == 1 else float(score)
+        if s >= 24:
+            return 32
+        if s >= 12:
+            return 16
+        if s >= 6.8:
+            return 8
+        return 4
+
+    # ------------------------------------------------------------------
+    # code storage pack / unpack / align (stquant_opt_simple.py:114-210)
+    # ------------------------------------------------------------------
+    @staticmethod
+    def _is_momentum_packed4(state):
+        if "exp_avg" not in state or "exp_avg_sq" not in state:
+            return False
+        ea, easq = state["exp_avg"], state["exp_avg_sq"]
+        return ea.dtype == torch.uint8 and easq.numel() == 0 and ea.numel() > 0
+
+    @staticmethod
+    def _unpack_packed4_momentum(state):
+        packed = state["exp_avg"]
+        m_u = (packed.to(torch.int32) & 0x0F).to(torch.int16)
+        v_q = ((packed.to(torch.int32) >> 4) & 0x0F).to(torch.int32)
+        state["exp_avg"] = (m_u - 8).to(torch.int8)
+        state["exp_avg_sq"] = v_q.to(torch.uint8)
+
+    @staticmethod
+    def _pack_momentum_to_nibbles(state):
+        ea, easq = state["exp_avg"], state["exp_avg_sq"]
+        if ea.dtype != torch.int8 or easq.numel() != ea.numel():
+            return
+        dev = ea.device
+        m_u = (ea.to(torch.int16) + 8).clamp(0, 15).to(torch.uint8)
+        v_lo = easq.to(torch.int32).clamp(0, 15).to(torch.uint8)
+        state["exp_avg"] = (m_u | (v_lo << 4)).to(dev)
+        state["exp_avg_sq"] = torch.empty(0, dtype=torch.uint8, device=dev)
+
+    @classmethod
+    def _align_momentum_storage(cls, state, bits):
+        if cls._is_momentum_packed4(state):
+            cls._unpack_packed4_momentum(state)
+
+        ea, easq = state["exp_avg"], state["exp_avg_sq"]
+
+        if bits >= 32:
+            if ea.dtype != torch.int32:
+                state["exp_avg"] = ea.to(torch.int32)
+            if easq.dtype != torch.uint32:
+                state["exp_avg_sq"] = easq.to(torch.uint32)
+            return
+
+        if bits > 8:
+            if ea.dtype == torch.int8:
+                state["exp_avg"] = ea.to(torch.int16)
+                state["exp_avg_sq"] = easq.to(torch.uint16)
+            elif ea.dtype == torch.int32:
+                state["exp_avg"] = ea.clamp(-32768, 32767).to(torch.int16)
+                state["exp_avg_sq"] = easq.to(torch.int64).clamp(0, 65535).to(torch.uint16)
+            elif ea.dtype != torch.int16:
+                state["exp_avg"] = ea.to(torch.int16)
+                state["exp_avg_sq"] = easq.to(torch.uint16)
+            return
+
+        if ea.dtype == torch.int16:
+            state["exp_avg"] = ea.clamp(-128, 127).to(torch.int8)
+            state["exp_avg_sq"] = easq.to(torch.int64).clamp(0, 255).to(torch.uint8)
+        elif ea.dtype == torch.int32:
+            state["exp_avg"] = ea.clamp(-128, 127).to(torch.int8)
+            state["exp_avg_sq"] = easq.to(torch.int64).clamp(0, 255).to(torch.uint8)
+        elif ea.dtype == torch.int8 and easq.numel() > 0 and easq.dtype != torch.uint8:
+            state["exp_avg_sq"] = easq.to(torch.uint8)
+
+    @classmethod
+    def _pack_momentum_storage(cls, state, bits):
+        ea, easq = state["exp_avg"], state["exp_avg_sq"]
+
+        if bits <= 8:
+            if ea.dtype == torch.int16:
+                state["exp_avg"] = ea.clamp(-128, 127).to(torch.int8)
+                state["exp_avg_sq"] = easq.to(torch.int64).clamp(0, 255).to(torch.uint8)
+            elif ea.dtype == torch.int32:
+                state["exp_avg"] = ea.clamp(-128, 127).to(torch.int8)
+                state["exp_avg_sq"] = easq.to(torch.int64).clamp(0, 255).to(torch.uint8)
+            elif ea.dtype == torch.int8 and easq.numel() > 0 and easq.dtype != torch.uint8:
+                state["exp_avg_sq"] = easq.to(torch.uint8)
+
+            if (
+                bits == 4
+                and state["exp_avg"].dtype == torch.int8
+                and state["exp_avg_sq"].numel() == state["exp_avg"].numel()
+            ):
+                cls._pack_momentum_to_nibbles(state)
+            return
+
+        if bits == 16:
+            if ea.dtype == torch.int32:
+                state["exp_avg"] = ea.clamp(-32768, 32767).to(torch.int16)
+                state["exp_avg_sq"] = easq.to(torch.int64).clamp(0, 65535).to(torch.uint16)
+            elif ea.dtype == torch.int8:
+                state["exp_avg"] = ea.to(torch.int16)
+                state["exp_avg_sq"] = easq.to(torch.uint16)
+            return
+
+        if bits >= 32:
+            if ea.dtype != torch.int32:
+                state["exp_avg"] = ea.to(torch.int32)
+            if easq.dtype != torch.uint32:
+                state["exp_avg_sq"] = easq.to(torch.uint32)
+
+    def _init_state_if_needed(self, p, state, block_size):
+        # stquant_opt_simple.py:212-225
+        if len(state) != 0:
+            return
+        state["step"] = 0
+        state["exp_avg"] = torch.zeros_like(p, dtype=torch.int16, memory_format=torch.contiguous_format)
+        state["exp_avg_sq"] = torch.zeros_like(p, dtype=torch.uint16, memory_format=torch.contiguous_format)
+        num_blocks = (p.numel() + block_size - 1) // block_size
+        state["scale_m"] = torch.zeros(num_blocks, dtype=torch.float32, device=p.device)
+        state["scale_v"] = torch.zeros(num_blocks, dtype=torch.float32, device=p.device)
+        state["v_min"] = torch.full((num_blocks,), -20.0, dtype=torch.float32, device=p.device)
+        state["current_bit"] = 16
+        state["last_score"] = torch.tensor(12.0, device=p.device)
+
+    def get_last_step_timings(self):
+        return dict(self.last_step_timings)
+
+    # ------------------------------------------------------------------
+    # per-tensor preparation around the batched kernel
+    # ------------------------------------------------------------------
+    def _prepare_update(self, p, group):
+        """Per-tensor work before the kernel: ``step += 1`` and the storage
+        alignment of stquant_opt_simple.py:231-239.  Returns True when the
+        storage must be re-packed after the kernel (:269).
+
+        A packed-nibble state at bits == 4 is handed to the packed kernel
+        directly: unpack -> int8/uint8 kernel -> re-pack (the reference's route)
+        yields the same codes, scales and params byte for byte.
+        """
+        state = self.state[p]
+        bits = int(state["current_bit"])
+        state["step"] += 1
+        if bits == 4 and self._is_momentum_packed4(state):
+            return False
+        self._align_momentum_storage(state, bits)
+        return True
+
+    def _finish_update(self, p):
+        state = self.state[p]
+        self._pack_momentum_storage(state, int(state["current_bit"]))
+
+    def _launch_fused_update(self, p, group):
+        """Single-tensor update with the reference's per-tensor timing (:231-280)."""
+        t0 = time.perf_counter()
+        repack = self._prepare_update(p, group)
+        unpack_ms = (time.perf_counter() - t0) * 1000.0
+        self._sync_device(p.device)
+        tk0 = time.perf_counter()
+        self._run_kernels([(p, group)])
+        self._sync_device(p.device)
+        kernel_ms = (time.perf_counter() - tk0) * 1000.0
+        t1 = time.perf_counter()
+        if repack:
+            self._finish_update(p)
+        pack_ms = (time.perf_counter() - t1) * 1000.0
+        lt = self.last_step_timings
+        lt["quant_dequant_unpack_ms"] = lt.get("quant_dequant_unpack_ms", 0.0) + unpack_ms
+        lt["quant_dequant_kernel_ms"] = lt.get("quant_dequant_kernel_ms", 0.0) + kernel_ms
+        lt["quant_dequant_pack_ms"] = lt.get("quant_dequant_pack_ms", 0.0) + pack_ms
+
+    def _run_kernels(self, items):
+        """Group tensors by (device, code storage, grad dtype, block size,
+        rounding, seed) and run one multi-tensor launch per group."""
+        buckets = OrderedDict()
+        for p, group in items:
+            state = self.state[p]
+            grad = p.grad
+            if grad.is_sparse:
+                raise RuntimeError("MDQAdamWSimple does not support sparse gradients")
+            if not grad.is_contiguous():
+                grad = grad.contiguous()
+            bsz = min(int(group["block_size"]), 1024)
+            rnd = mdq_hip.rounding_code(group.get("rounding", "nearest"))
+            seed = int(group.get("seed", 0) or 0)
+            ea, easq = state["exp_avg"], state["exp_avg_sq"]
+            key = (p.device, ea.dtype, easq.dtype, easq.numel() == 0, grad.dtype, bsz, rnd, seed)
+            b1, b2 = group["betas"]
+            buckets.setdefault(key, []).append(mdq_hip.TensorState(
+                p=p, grad=grad, exp_avg=ea, exp_avg_sq=easq, scale_m=state["scale_m"],
+                scale_v=state["scale_v"], v_min=state["v_min"], step=state["step"],
+                bits=int(state["current_bit"]), lr=group["lr"], beta1=b1, beta2=b2, eps=group["eps"],
+                weight_decay=group["weight_decay"], tensor_id=self._tensor_ids.get(p, 0)))
+        for (dev, _ea, _easq, _packed, _gdt, bsz, rnd, seed), entries in buckets.items():
+            prof = None
+            if self._kernel_profile_buf is not None and self._kernel_profile_device == dev:
+                prof = self._kernel_profile_buf
+            mdq_hip.multi_tensor_step(entries, bsz, rounding=rnd, seed=seed, profile_cycles=prof)
+
+    @property
+    def _tensor_ids(self):
+        ids = getattr(self, "_tensor_id_cache", None)
+        if ids is None or len(ids) != sum(len(g["params"]) for g in self.param_groups):
+            ids = {}
+            k = 0
+            for g in self.param_groups:
+                for p in g["params"]:
+                    ids[p] = k
+                    k += 1
+            self._tensor_id_cache = ids
+        return ids
+
+    def _finalize_step_timings(self, profile_device):
+        # stquant_opt_simple.py:282-316
+        unpack = self.last_step_timings.get("quant_dequant_unpack_ms", 0.0)
+        pack = self.last_step_timings.get("quant_dequant_pack_ms", 0.0)
+        kernel_wall = self.last_step_timings.get("quant_dequant_kernel_ms", 0.0)
+
+        self.last_step_timings["mdq_unpack_ms"] = unpack
+        self.last_step_timings["mdq_pack_ms"] = pack
+        self.last_step_timings["mdq_fused_kernel_ms"] = kernel_wall
+        self.last_step_timings["mdq_quant_dequant_ms"] = unpack + kernel_wall + pack
+
+        if profile_device is not None:
+            k_ms = self._kernel_phases_ms_from_wall(profile_device, kernel_wall)
+            (
+                self.last_step_timings["mdq_kernel_dequant_ms"],
+                self.last_step_timings["mdq_kernel_adam_mv_ms"],
+                self.last_step_timings["mdq_kernel_scale_reduce_ms"],
+                self.last_step_timings["mdq_kernel_quant_ms"],
+                self.last_step_timings["mdq_kernel_update_p_ms"],
+            ) = k_ms
+            self.last_step_timings["mdq_kernel_phases_sum_ms"] = sum(k_ms)
+            self.last_step_timings["mdq_kernel_profile_cycles"] = self._read_kernel_profile_cycles(profile_device)
+        else:
+            for key in (
+                "mdq_kernel_dequant_ms",
+                "mdq_kernel_adam_mv_ms",
+                "mdq_kernel_scale_reduce_ms",
+                "mdq_kernel_quant_ms",
+                "mdq_kernel_update_p_ms",
+                "mdq_kernel_phases_sum_ms",
+                "mdq_kernel_profile_cycles",
+            ):
+                self.last_step_timings[key] = 0.0 if key != "mdq_kernel_profile_cycles" else []
+
+    # ------------------------------------------------------------------
+    # metrics / checkpoint (stquant_opt_simple.py:321-378)
+    # ------------------------------------------------------------------
+    def get_bit_distribution(self):
+        counts = {4: 0, 8: 0, 16: 0, 32: 0}
+        num_tensors = 0
+        for group in self.param_groups:
+            for p in group["params"]:
+                st = self.state.get(p)
+                if st and "current_bit" in st:
+                    b = int(st["current_bit"])
+                    counts[b] = counts.get(b, 0) + 1
+                    num_tensors += 1
+        if num_tensors == 0:
+            return {4: 0.0, 8: 0.0, 16: 0.0, 32: 0.0}
+        return {b: (c / num_tensors) * 100.0 for b, c in counts.items()}
+
+    def get_bit_distribution_param_weighted(self):
+        counts_numel = {4: 0, 8: 0, 16: 0, 32: 0}
+        for group in self.param_groups:
+            for p in group["params"]:
+                st = self.state.get(p)
+                if st and "current_bit" in st:
+                    b = int(st["current_bit"])
+                    counts_numel[b] = counts_numel.get(b, 0) + p.numel()
+        total = sum(counts_numel.values())
+        if total == 0:
+            return {4: 0.0, 8: 0.0, 16: 0.0, 32: 0.0}
+        return {k: (v / total) * 100.0 for k, v in counts_numel.items()}
+
+    def get_avg_bit_param_weighted(self):
+        dist_bits = self.get_bit_distribution_param_weighted()
+        return float(sum(b * (perc / 100.0) for b, perc in dist_bits.items()))
+
+    def get_all_raw_scores(self):
+        scores = []
+        for group in self.param_groups:
+            for p in group["params"]:
+                st = self.state.get(p)
+                if st and "last_score" in st:
+                    scores.append(float(st["last_score"].item()))
+        return scores
+
+    def state_dict(self):
+        out = super().state_dict()
+        out["mdq_global_stats"] = {
+            "n_ema": self.n_ema,
+            "r_ema": self.r_ema,
+            "v_global_ema": self.v_global_ema,
+            "total_steps": self.total_steps,
+        }
+        return out
+
+    _CODE_KEYS = ("exp_avg", "exp_avg_sq")
+
+    def load_state_dict(self, state_dict):
+        """As stquant_opt_simple.py:371-378, plus the repair the reference lacks:
+        torch's ``Optimizer.load_state_dict`` casts every floating-point-param
+        state tensor to the param dtype, turning integer codes into float32.
+        The code values are small integers (exact in float32); each code tensor
+        is cast back to the integer dtype it had in ``state_dict``."""
+        saved_dtypes = {}
+        for pid, st in state_dict.get("state", {}).items():
+            saved_dtypes[pid] = {k: st[k].dtype for k in self._CODE_KEYS
+                                 if k in st and torch.is_tensor(st[k])}
+        state_dict = dict(state_dict)
+        if "mdq_global_stats" in state_dict:
+            stats = state_dict.pop("mdq_global_stats")
+            self.n_ema = stats["n_ema"]
+            self.r_ema = stats["r_ema"]
+            self.v_global_ema = stats["v_global_ema"]
+            self.total_steps = stats["total_steps"]
+        super().load_state_dict(state_dict)
+        params = [p for g in self.param_groups for p in g["params"]]
+        saved_ids = [pid for g in state_dict["param_groups"] for pid in g["params"]]
+        for pid, p in zip(saved_ids, params):
+            st = self.state.get(p)
+            if not st:
+                continue
+            for k, dt in saved_dtypes.get(pid, {}).items():
+                if st[k].dtype != dt:
+                    st[k] = st[k].to(dt)
+
+    # ------------------------------------------------------------------
+    # step (stquant_opt_simple.py:383-508)
+    # ------------------------------------------------------------------
+    @torch.no_grad()
+    def step(self, closure=None):
+        loss = None
+        if closure is not None:
+            with torch.enable_grad():
+                loss = closure()
+
+        self.total_steps += 1
+        self.last_step_timings = {
+            "mdq_stats_ms": 0.0,
+            "mdq_bit_decision_ms": 0.0,
+            "mdq_grad_stats_ms": 0.0,
+            "mdq_allreduce_ms": 0.0,
+            "mdq_score_bits_ms": 0.0,
+            "mdq_update_decision": False,
+            "mdq_update_freq": 0,
+            "quant_dequant_unpack_ms": 0.0,
+            "quant_dequant_kernel_ms": 0.0,
+            "quant_dequant_pack_ms": 0.0,
+            "mdq_fused_io_fast_path_params": 0,
+            "mdq_fused_io_fallback_params": 0,
+        }
+
+        update_freq = self.param_groups[0]["update_freq"]
+        update_decision = (self.total_steps % update_freq == 0) or (self.total_steps < 5)
+        self.last_step_timings["mdq_update_decision"] = update_decision
+        self.last_step_timings["mdq_update_freq"] = update_freq
+
+        params_with_grad = []
+        all_stats = []
+
+        for group in self.param_groups:
+            b_size = min(int(group.get("block_size", 256)), 1024)
+            for p in group["params"]:
+                if p.grad is None:
+                    continue
+                params_with_grad.append((p, group))
+                state = self.state[p]
+                self._init_state_if_needed(p, state, b_size)
+
+        # Fixed-width groups (new ``bits`` option) skip the score.
+        for p, group in params_with_grad:
+            if group.get("bits") is not None:
+                self.state[p]["current_bit"] = int(group["bits"])
+        scored = all(g.get("bits") is None for _p, g in params_with_grad)
+
+        grad_stats_ms = 0.0
+        allreduce_ms = 0.0
+        score_bits_ms = 0.0
+
+        if update_decision and params_with_grad and scored:
+            dev = params_with_grad[0][0].device
+            self._sync_device(dev)
+            t_grad = time.perf_counter()
+            for p, _group in params_with_grad:
+                all_stats.append(self._compute_grad_stats(p.grad.float()))
+            self._sync_device(dev)
+            grad_stats_ms = (time.perf_counter() - t_grad) * 1000.0
+
+        if update_decision and all_stats:
+            dev = params_with_grad[0][0].device
+            stats_tensor = torch.stack(all_stats)
+            avg_stats = stats_tensor.mean(dim=0)
+
+            if dist.is_available() and dist.is_initialized():
+                self._sync_device(dev)
+                t_ar = time.perf_counter()
+                dist.all_reduce(avg_stats, op=dist.ReduceOp.SUM)
+                avg_stats /= dist.get_world_size()
+                self._sync_device(dev)
+                allreduce_ms = (time.perf_counter() - t_ar) * 1000.0
+
+            self._sync_device(dev)
+            t_score = time.perf_counter()
+            if self.n_ema is None:
+                self.n_ema = avg_stats[0]
+                self.r_ema = avg_stats[1]
+                self.v_global_ema = avg_stats[2]
+            else:
+                alpha = self.param_groups[0]["alpha"]
+                self.n_ema = alpha * avg_stats[0] + (1 - alpha) * self.n_ema
+                self.r_ema = alpha * avg_stats[1] + (1 - alpha) * self.r_ema
+                self.v_global_ema = alpha * avg_stats[2] + (1 - alpha) * self.v_global_ema
+
+            tau = self.param_groups[0]["tau"]
+            for i, (p, _group) in enumerate(params_with_grad):
+                state = self.state[p]
+                n_l, r_l, v_l = stats_tensor[i]
+                s_t = 1.0 + (
+                    1.0 / torch.cosh(torch.tensor(state["step"] / tau, device=p.device, dtype=torch.float32))
+                )
+                score = (
+                    7.2
+                    + torch.log2(r_l / (self.r_ema + 1e-12))
+                    + torch.log2(n_l / (self.n_ema + 1e-12))
+                    + torch.log2(s_t)
+                    + torch.log2(v_l / (self.v_global_ema + 1e-12))
+                )
+                state["last_score"] = score
+                state["current_bit"] = self._score_to_bits(score)
+            self._sync_device(dev)
+            score_bits_ms = (time.perf_counter() - t_score) * 1000.0
+
+        lt = self.last_step_timings
+        lt["mdq_grad_stats_ms"] = grad_stats_ms
+        lt["mdq_allreduce_ms"] = allreduce_ms
+        lt["mdq_score_bits_ms"] = score_bits_ms
+        lt["mdq_stats_ms"] = grad_stats_ms
+        lt["mdq_bit_decision_ms"] = allreduce_ms + score_bits_ms
+        lt["mdq_extra_stats_ms"] = grad_stats_ms + allreduce_ms + score_bits_ms
+
+        profile_device = None
+        if params_with_grad:
+            profile_device = params_with_grad[0][0].device
+            if profile_device.type == "cuda":
+                self._reset_kernel_profile(profile_device)
+
+        if params_with_grad:
+            self._batched_update(params_with_grad)
+
+        self._finalize_step_timings(
+            profile_device if profile_device is not None and profile_device.type == "cuda" else None
+        )
+        return loss
+
+    def _batched_update(self, params_with_grad):
+        """All tensors: prepare (align storage), one launch per storage class,
+        re-pack; timing keys as the per-tensor loop of :501-502 fills them."""
+        dev = params_with_grad[0][0].device
+        t0 = time.perf_counter()
+        repack = [self._prepare_update(p, g) for p, g in params_with_grad]
+        unpack_ms = (time.perf_counter() - t0) * 1000.0
+        if self.sync_timing:
+            self._sync_device(dev)
+        tk0 = time.perf_counter()
+        self._run_kernels(params_with_grad)
+        if self.sync_timing:
+            self._sync_device(dev)
+        kernel_ms = (time.perf_counter() - tk0) * 1000.0
+        t1 = time.perf_counter()
+        for (p, _g), rp in zip(params_with_grad, repack):
+            if rp:
+                self._finish_update(p)
+        pack_ms = (time.perf_counter() - t1) * 1000.0
+        lt = self.last_step_timings
+        lt["quant_dequant_unpack_ms"] += unpack_ms
+        lt["quant_dequant_kernel_ms"] += kernel_ms
+        lt["quant_dequant_pack_ms"] += pack_ms

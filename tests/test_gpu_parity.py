@@ -1,0 +1,290 @@
+"""GPU parity: the HIP kernels (through the C ABI) against the CPU oracle.
+
+Bar: packed codes, int codes and the three block-scale arrays bit-exact;
+params within 1e-6 relative (per element: |dp| <= 1e-6 * (|p| + |update|),
+and max|dp| <= 1e-6 * max|p|), because the device update uses the hardware
+sqrt/reciprocal while the oracle uses IEEE sqrtf and division.
+"""
+import numpy as np
+import pytest
+import torch
+
+import mdq_hip
+from oracle import mdq_oracle as orc
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+HP = dict(beta1=0.9, beta2=0.999, lr=1e-3, weight_decay=0.01, eps=1e-8)
+STORE_TORCH = {
+    orc.STORE_P4: (torch.uint8, None),
+    orc.STORE_S8: (torch.int8, torch.uint8),
+    orc.STORE_S16: (torch.int16, torch.uint16),
+    orc.STORE_S32: (torch.int32, torch.uint32),
+}
+
+
+def to_dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def assert_bits_equal(name, t, a):
+    got = t.cpu().numpy()
+    if got.dtype == np.float32:
+        ok = np.array_equal(got.view(np.uint32), a.view(np.uint32))
+    else:
+        ok = np.array_equal(got, a)
+    if not ok:
+        bad = np.nonzero(got.view(np.uint8 if got.dtype.itemsize == 1 else got.dtype) != a.view(got.dtype))[0]
+        raise AssertionError(f"{name}: {bad.size} mismatches, first at {bad[:5]} got {got[bad[:5]]} want {a[bad[:5]]}")
+
+
+def assert_params_close(p_gpu, p_ref, p_prev):
+    got = p_gpu.cpu().numpy().astype(np.float64)
+    ref = p_ref.astype(np.float64)
+    upd = np.abs(ref - p_prev.astype(np.float64))
+    err = np.abs(got - ref)
+    assert np.all(err <= 1e-6 * (np.abs(ref) + upd) + 1e-30), f"max elementwise excess {np.max(err - 1e-6 * (np.abs(ref) + upd))}"
+    assert err.max() <= 1e-6 * np.abs(ref).max()
+
+
+class Case:
+    """One tensor's numpy state (oracle side) and torch state (device side)."""
+
+    def __init__(self, n, B, storage, rng, grad_dtype=np.float32, offset=0):
+        self.n, self.B, self.storage = n, B, storage
+        self.p = (rng.standard_normal(n) * 0.02).astype(np.float32)
+        self.state = list(orc.init_state(n, B, storage))
+        self.offset = offset
+        # device copies; `offset` elements of padding in front make the views unaligned
+        self.tp = self._dev_view(self.p)
+        cm, cv = self.state[0], self.state[1]
+        self.tcm = self._dev_view(cm)
+        self.tcv = self._dev_view(cv) if cv is not None else torch.empty(0, dtype=torch.uint8, device=DEV)
+        self.tsm, self.tsv, self.tvm = (to_dev(a.copy()) for a in self.state[2:])
+        self.grad_dtype = grad_dtype
+
+    def _dev_view(self, a):
+        if self.offset == 0:
+            return to_dev(a.copy())
+        buf = np.zeros(a.size + self.offset, dtype=a.dtype)
+        buf[self.offset:] = a
+        return to_dev(buf)[self.offset:]
+
+    def grads(self, rng):
+        g = (rng.standard_normal(self.n) * 1e-3).astype(np.float32)
+        if self.grad_dtype == "bf16":
+            tg = torch.from_numpy(g).to(torch.bfloat16)
+            g_np = tg.view(torch.int16).numpy().view(np.uint16).copy()
+            return g_np, self._dev_view_t(tg)
+        if self.grad_dtype == np.float16:
+            g16 = g.astype(np.float16)
+            return g16, self._dev_view(g16)
+        return g, self._dev_view(g)
+
+    def _dev_view_t(self, t):
+        if self.offset == 0:
+            return t.to(DEV)
+        buf = torch.zeros(t.numel() + self.offset, dtype=t.dtype)
+        buf[self.offset:] = t
+        return buf.to(DEV)[self.offset:]
+
+    def oracle_step(self, g, step, bits, **kw):
+        hp = dict(HP)
+        hp.update(kw)
+        cm, cv, sm, sv, vm = self.state
+        orc.step(self.p, g, cm, cv, sm, sv, vm, step=step, bits=bits, block_size=self.B,
+                 storage=self.storage, **hp)
+
+    def entry(self, tg, step, bits, tensor_id=0, **kw):
+        hp = dict(HP)
+        hp.update(kw)
+        return mdq_hip.TensorState(self.tp, tg, self.tcm, self.tcv, self.tsm, self.tsv, self.tvm, step, bits,
+                                   hp["lr"], hp["beta1"], hp["beta2"], hp["eps"], hp["weight_decay"],
+                                   tensor_id)
+
+    def check(self, p_prev):
+        torch.cuda.synchronize()
+        cm, cv, sm, sv, vm = self.state
+        assert_bits_equal("exp_avg", self.tcm, cm)
+        if cv is not None:
+            assert_bits_equal("exp_avg_sq", self.tcv, cv)
+        assert_bits_equal("scale_m", self.tsm, sm)
+        assert_bits_equal("scale_v", self.tsv, sv)
+        assert_bits_equal("v_min", self.tvm, vm)
+        assert_params_close(self.tp, self.p, p_prev)
+
+
+def test_config1_flat_4m_packed4_ten_steps():
+    """4,194,304 fp32 params ~N(0,0.02), fp32 grads ~N(0,1e-3)
+    redrawn each step from seed 0; 4-bit, B=128, nearest; 10 steps, compared after each."""
+    print("case: config1 n=4194304 B=128 packed4 nearest", flush=True)
+    n, B = 4_194_304, 128
+    gen = torch.Generator().manual_seed(0)
+    p0 = (torch.randn(n, generator=gen) * 0.02).numpy()
+    st = list(orc.init_state(n, B, orc.STORE_P4))
+    p = p0.copy()
+    tp = to_dev(p0.copy())
+    tcm = to_dev(st[0].copy())
+    tsm, tsv, tvm = (to_dev(a.copy()) for a in st[2:])
+    empty = torch.empty(0, dtype=torch.uint8, device=DEV)
+    for step in range(1, 11):
+        g = (torch.randn(n, generator=gen) * 1e-3).numpy()
+        p_prev = p.copy()
+        orc.step(p, g, st[0], None, st[2], st[3], st[4], step=step, bits=4, block_size=B,
+                 storage=orc.STORE_P4, **HP)
+        mdq_hip.fused_step(tp, to_dev(g), tcm, empty, tsm, tsv, tvm, HP["beta1"], HP["beta2"], HP["lr"],
+                           HP["weight_decay"], HP["eps"], step, 4, B)
+        torch.cuda.synchronize()
+        assert_bits_equal(f"step {step} codes", tcm, st[0])
+        assert_bits_equal(f"step {step} scale_m", tsm, st[2])
+        assert_bits_equal(f"step {step} scale_v", tsv, st[3])
+        assert_bits_equal(f"step {step} v_min", tvm, st[4])
+        assert_params_close(tp, p, p_prev)
+
+
+STORAGE_BITS = [(orc.STORE_P4, 4), (orc.STORE_S8, 4), (orc.STORE_S8, 8), (orc.STORE_S16, 16),
+                (orc.STORE_S16, 8), (orc.STORE_S32, 32), (orc.STORE_S32, 16)]
+
+
+@pytest.mark.parametrize("storage,bits", STORAGE_BITS)
+@pytest.mark.parametrize("B", [64, 128, 256])
+def test_storage_and_block_sizes(storage, bits, B):
+    print(f"case: storage={storage} bits={bits} B={B}", flush=True)
+    rng = np.random.default_rng(1000 * storage + 10 * bits + B)
+    c = Case(B * 37 + 19, B, storage, rng)
+    for step in (1, 2, 3):
+        g, tg = c.grads(rng)
+        p_prev = c.p.copy()
+        c.oracle_step(g, step, bits)
+        mdq_hip.multi_tensor_step([c.entry(tg, step, bits)], B)
+        c.check(p_prev)
+
+
+@pytest.mark.parametrize("B", [1, 2, 4, 8, 16, 32, 512, 1024])
+def test_all_block_sizes(B):
+    print(f"case: block size {B}", flush=True)
+    rng = np.random.default_rng(B)
+    for storage, bits in ((orc.STORE_P4, 4), (orc.STORE_S8, 8)):
+        c = Case(B * 23 + max(1, B // 3), B, storage, rng)
+        for step in (1, 2):
+            g, tg = c.grads(rng)
+            p_prev = c.p.copy()
+            c.oracle_step(g, step, bits)
+            mdq_hip.multi_tensor_step([c.entry(tg, step, bits)], B)
+            c.check(p_prev)
+
+
+@pytest.mark.parametrize("gdt", ["bf16", np.float16])
+def test_low_precision_grads(gdt):
+    print(f"case: grad dtype {gdt}", flush=True)
+    rng = np.random.default_rng(5)
+    c = Case(128 * 100 + 3, 128, orc.STORE_P4, rng, grad_dtype=gdt)
+    for step in (1, 2, 3):
+        g, tg = c.grads(rng)
+        p_prev = c.p.copy()
+        c.oracle_step(g, step, 4)
+        mdq_hip.multi_tensor_step([c.entry(tg, step, 4)], 128)
+        c.check(p_prev)
+
+
+def test_unaligned_views_take_the_guarded_path():
+    print("case: unaligned views", flush=True)
+    rng = np.random.default_rng(6)
+    c = Case(128 * 50, 128, orc.STORE_S8, rng, offset=1)
+    for step in (1, 2):
+        g, tg = c.grads(rng)
+        p_prev = c.p.copy()
+        c.oracle_step(g, step, 8)
+        mdq_hip.multi_tensor_step([c.entry(tg, step, 8)], 128)
+        c.check(p_prev)
+
+
+@pytest.mark.parametrize("storage,bits", [(orc.STORE_P4, 4), (orc.STORE_S8, 8), (orc.STORE_S16, 16)])
+def test_stochastic_rounding_bit_exact(storage, bits):
+    print(f"case: stochastic storage={storage} bits={bits}", flush=True)
+    rng = np.random.default_rng(7)
+    c = Case(128 * 64 + 77, 128, storage, rng)
+    for step in (1, 2, 3):
+        g, tg = c.grads(rng)
+        p_prev = c.p.copy()
+        c.oracle_step(g, step, bits, rounding=orc.ROUND_STOCHASTIC, seed=1234, tensor_id=9)
+        mdq_hip.multi_tensor_step([c.entry(tg, step, bits, tensor_id=9)], 128,
+                                  rounding="stochastic", seed=1234)
+        c.check(p_prev)
+
+
+def test_multi_tensor_ragged_heavy_tail():
+    """Config-5-style: many tensors with log-uniform sizes (mostly not multiples of B),
+    Student-t grads with all-zero blocks and x1000 outliers, per-tensor steps and
+    hyper-parameters, one launch."""
+    print("case: ragged multi-tensor", flush=True)
+    rng = np.random.default_rng(0)
+    sizes = np.clip(np.floor(np.exp(rng.uniform(0, np.log(2 ** 17), 41))), 1, 2 ** 17).astype(int)
+    B = 128
+    cases = [Case(int(s), B, orc.STORE_P4, rng) for s in sizes]
+    for step in (1, 2):
+        entries, prevs = [], []
+        for i, c in enumerate(cases):
+            g = (rng.standard_t(3, c.n) * 1e-3).astype(np.float32)
+            nb = (c.n + B - 1) // B
+            zero_blocks = rng.random(nb) < 0.05
+            g[np.repeat(zero_blocks, B)[: c.n]] = 0.0
+            out = rng.random(c.n) < 0.001
+            g[out] *= 1000.0
+            lr = 1e-3 * (1 + i % 3)
+            prevs.append(c.p.copy())
+            c.oracle_step(g, step + i % 2, 4, lr=lr)
+            entries.append(c.entry(to_dev(g), step + i % 2, 4, tensor_id=i, lr=lr))
+        mdq_hip.multi_tensor_step(entries, B)
+        for c, pp in zip(cases, prevs):
+            c.check(pp)
+
+
+def test_determinism_across_calls():
+    rng = np.random.default_rng(8)
+    n, B = 128 * 300 + 5, 128
+    p = torch.from_numpy((rng.standard_normal(n) * 0.02).astype(np.float32)).to(DEV)
+    g = torch.from_numpy((rng.standard_normal(n) * 1e-3).astype(np.float32)).to(DEV)
+    outs = []
+    for _ in range(2):
+        cm, _cv, sm, sv, vm = orc.init_state(n, B, orc.STORE_P4)
+        t = [p.clone(), to_dev(cm), to_dev(sm), to_dev(sv), to_dev(vm)]
+        mdq_hip.fused_step(t[0], g, t[1], torch.empty(0, dtype=torch.uint8, device=DEV), t[2], t[3], t[4],
+                           0.9, 0.999, 1e-3, 0.01, 1e-8, 1, 4, B)
+        outs.append([x.cpu() for x in t])
+    for a, b in zip(*outs):
+        assert torch.equal(a, b)
+
+
+def test_profile_cycles_accumulate():
+    rng = np.random.default_rng(9)
+    n, B = 128 * 1000, 128
+    c = Case(n, B, orc.STORE_P4, rng)
+    g, tg = c.grads(rng)
+    prof = torch.zeros(5, dtype=torch.int64, device=DEV)
+    mdq_hip.multi_tensor_step([c.entry(tg, 1, 4)], B, profile_cycles=prof)
+    p_prev = c.p.copy()
+    c.oracle_step(g, 1, 4)
+    c.check(p_prev)
+    cyc = prof.cpu().numpy()
+    assert np.all(cyc > 0), cyc
+
+
+def test_errors_follow_the_reference_messages():
+    p = torch.zeros(256, device=DEV)
+    g = torch.zeros(256, device=DEV)
+    sm = torch.zeros(2, device=DEV)
+    bad_ea = torch.zeros(256, dtype=torch.int16, device=DEV)
+    bad_easq = torch.zeros(256, dtype=torch.uint8, device=DEV)
+    with pytest.raises(RuntimeError, match="MDQ: state must be packed4"):
+        mdq_hip.fused_step(p, g, bad_ea, bad_easq, sm, sm.clone(), sm.clone(), 0.9, 0.999, 1e-3, 0.0, 1e-8, 1, 4, 128)
+    with pytest.raises(RuntimeError, match="packed4: exp_avg numel must match parameters"):
+        mdq_hip.fused_step(p, g, torch.zeros(255, dtype=torch.uint8, device=DEV),
+                           torch.empty(0, dtype=torch.uint8, device=DEV), sm, sm.clone(), sm.clone(),
+                           0.9, 0.999, 1e-3, 0.0, 1e-8, 1, 4, 128)
+    with pytest.raises(RuntimeError, match="p/grad must be CUDA"):
+        mdq_hip.fused_step(p.cpu(), g, bad_ea, bad_easq, sm, sm, sm, 0.9, 0.999, 1e-3, 0.0, 1e-8, 1, 4, 128)
+    with pytest.raises(RuntimeError, match="profile_cycles needs >= 5 elements"):
+        mdq_hip.fused_step(p, g, torch.full((256,), 8, dtype=torch.uint8, device=DEV),
+                           torch.empty(0, dtype=torch.uint8, device=DEV), sm, sm.clone(), sm.clone(),
+                           0.9, 0.999, 1e-3, 0.0, 1e-8, 1, 4, 128, torch.zeros(3, dtype=torch.int64, device=DEV))
