@@ -148,6 +148,8 @@ def main():
     ap.add_argument("--config", default="llama7b", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-gib", type=float, default=0.0,
+                    help="also run a plain device-to-device copy of this many GiB (rocprof calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the step shards by quant block across GPUs "
@@ -185,6 +187,16 @@ def main():
     wall = time.perf_counter() - t0
     kernel_ms = ev0.elapsed_time(ev1) / args.steps
     log(f"timed {args.steps} steps: {kernel_ms:.3f} ms/step (events), wall {wall / args.steps * 1e3:.3f} ms/step")
+
+    if args.copy_gib > 0:
+        n = int(args.copy_gib * (1 << 30)) // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy calibration: 3 x {n * 4} bytes read + written")
+        del src, dst
 
     N = w["N"]
     bpp = bytes_per_param(w["grad_bytes"], w["bits"], w["B"])

@@ -39,12 +39,22 @@ def assert_bits_equal(name, t, a):
 
 
 def assert_params_close(p_gpu, p_ref, p_prev):
+    """One step from identical inputs: |dp| <= 1e-6 (|p| + |update|) per element."""
     got = p_gpu.cpu().numpy().astype(np.float64)
     ref = p_ref.astype(np.float64)
     upd = np.abs(ref - p_prev.astype(np.float64))
     err = np.abs(got - ref)
-    assert np.all(err <= 1e-6 * (np.abs(ref) + upd) + 1e-30), f"max elementwise excess {np.max(err - 1e-6 * (np.abs(ref) + upd))}"
+    tol = 1e-6 * (np.abs(ref) + upd) + 1e-30
+    if not np.all(err <= tol):
+        i = int(np.argmax(err / tol))
+        raise AssertionError(f"param {i}: got {got[i]!r} want {ref[i]!r} prev {p_prev[i]!r} "
+                             f"err {err[i]:.3e} update {upd[i]:.3e} ({err[i] / max(upd[i], 1e-300):.2e} of it)")
     assert err.max() <= 1e-6 * np.abs(ref).max()
+
+
+def resync_params(tp, p):
+    """Start the next step from the oracle's params so each step is judged alone."""
+    tp.copy_(torch.from_numpy(p))
 
 
 class Case:
@@ -112,6 +122,7 @@ class Case:
         assert_bits_equal("scale_v", self.tsv, sv)
         assert_bits_equal("v_min", self.tvm, vm)
         assert_params_close(self.tp, self.p, p_prev)
+        resync_params(self.tp, self.p)
 
 
 def test_config1_flat_4m_packed4_ten_steps():
@@ -140,6 +151,29 @@ def test_config1_flat_4m_packed4_ten_steps():
         assert_bits_equal(f"step {step} scale_v", tsv, st[3])
         assert_bits_equal(f"step {step} v_min", tvm, st[4])
         assert_params_close(tp, p, p_prev)
+        resync_params(tp, p)
+
+
+def test_config1_accumulated_param_drift():
+    """Without re-syncing, 10 steps of independent roundoff stay within 1e-6 of max|p|."""
+    n, B = 1 << 20, 128
+    gen = torch.Generator().manual_seed(0)
+    p = (torch.randn(n, generator=gen) * 0.02).numpy()
+    st = list(orc.init_state(n, B, orc.STORE_P4))
+    tp = to_dev(p.copy())
+    tcm = to_dev(st[0].copy())
+    tsm, tsv, tvm = (to_dev(a.copy()) for a in st[2:])
+    empty = torch.empty(0, dtype=torch.uint8, device=DEV)
+    for step in range(1, 11):
+        g = (torch.randn(n, generator=gen) * 1e-3).numpy()
+        orc.step(p, g, st[0], None, st[2], st[3], st[4], step=step, bits=4, block_size=B,
+                 storage=orc.STORE_P4, **HP)
+        mdq_hip.fused_step(tp, to_dev(g), tcm, empty, tsm, tsv, tvm, HP["beta1"], HP["beta2"], HP["lr"],
+                           HP["weight_decay"], HP["eps"], step, 4, B)
+    torch.cuda.synchronize()
+    assert_bits_equal("codes", tcm, st[0])
+    err = np.abs(tp.cpu().numpy().astype(np.float64) - p)
+    assert err.max() <= 1e-6 * np.abs(p).max()
 
 
 STORAGE_BITS = [(orc.STORE_P4, 4), (orc.STORE_S8, 4), (orc.STORE_S8, 8), (orc.STORE_S16, 16),
