@@ -59,17 +59,6 @@ const char *dtype_name(int dt)
     }
 }
 
-int elem_bytes(int dt)
-{
-    switch (dt) {
-    case STQ_FLOAT: case STQ_INT: case STQ_UINT32: return 4;
-    case STQ_BFLOAT16: case STQ_HALF: case STQ_SHORT: case STQ_UINT16: return 2;
-    case STQ_BYTE: case STQ_CHAR: return 1;
-    case STQ_LONG: return 8;
-    default: return 0;
-    }
-}
-
 // Storage dispatch of stquant_kernel.cu:430-464.  Returns the storage class or
 // -1 (message set).  packed4 needs bits == 4, uint8 m codes, empty v codes.
 int pick_storage(int bits, int ea_dt, int64_t ea_numel, int easq_dt, int64_t easq_numel, int64_t numel)
@@ -169,10 +158,12 @@ int make_desc(const stq_tensor &t, int storage, int grad_dt, int B, MdqDesc &d)
 }
 
 // ----------------------------------------------------- per-device resources
+// A device buffer holding n MdqDesc followed by n int64 tile starts, and its
+// pinned host staging copy.
 struct Slot {
-    MdqDesc *dev = nullptr;
-    MdqDesc *host = nullptr;
-    size_t cap = 0;
+    char *dev = nullptr;
+    char *host = nullptr;
+    size_t cap = 0;   // bytes
     hipEvent_t done = nullptr;
     bool pending = false;
 };
@@ -204,17 +195,6 @@ int get_ctx(DevCtx **out)
     return STQ_OK;
 }
 
-// Workgroups per CU of the persistent grid (env STQ_WG_PER_CU overrides).
-int wg_per_cu()
-{
-    static int v = [] {
-        const char *s = std::getenv("STQ_WG_PER_CU");
-        int x = s ? std::atoi(s) : 0;
-        return x > 0 ? x : 8;
-    }();
-    return v;
-}
-
 // Uploads descs to a device slot on `stream` and launches.  The slot's pinned
 // staging buffer is reused only after the event recorded behind its previous
 // launch has completed.
@@ -233,15 +213,16 @@ int upload_and_launch(const std::vector<MdqDesc> &descs, int storage, int grad_d
         if (e != hipSuccess) return hip_fail(e, "hipEventSynchronize");
         s.pending = false;
     }
-    const size_t need = descs.size();
+    const size_t n = descs.size();
+    const size_t need = n * (sizeof(MdqDesc) + sizeof(long long));
     if (s.cap < need) {
         if (s.dev) { (void)hipFree(s.dev); s.dev = nullptr; }
         if (s.host) { (void)hipHostFree(s.host); s.host = nullptr; }
         s.cap = 0;
-        size_t cap = need < 64 ? 64 : need + need / 2;
-        e = hipMalloc((void **)&s.dev, cap * sizeof(MdqDesc));
+        size_t cap = need < 16384 ? 16384 : need + need / 2;
+        e = hipMalloc((void **)&s.dev, cap);
         if (e != hipSuccess) return hip_fail(e, "hipMalloc(descriptors)");
-        e = hipHostMalloc((void **)&s.host, cap * sizeof(MdqDesc), hipHostMallocDefault);
+        e = hipHostMalloc((void **)&s.host, cap, hipHostMallocDefault);
         if (e != hipSuccess) return hip_fail(e, "hipHostMalloc(descriptors)");
         s.cap = cap;
     }
@@ -249,18 +230,20 @@ int upload_and_launch(const std::vector<MdqDesc> &descs, int storage, int grad_d
         e = hipEventCreateWithFlags(&s.done, hipEventDisableTiming);
         if (e != hipSuccess) return hip_fail(e, "hipEventCreate");
     }
-    std::memcpy(s.host, descs.data(), need * sizeof(MdqDesc));
-    e = hipMemcpyAsync(s.dev, s.host, need * sizeof(MdqDesc), hipMemcpyHostToDevice, stream);
+    std::memcpy(s.host, descs.data(), n * sizeof(MdqDesc));
+    long long *tb = reinterpret_cast<long long *>(s.host + n * sizeof(MdqDesc));
+    for (size_t i = 0; i < n; ++i) tb[i] = descs[i].tile_begin;
+    e = hipMemcpyAsync(s.dev, s.host, need, hipMemcpyHostToDevice, stream);
     if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(descriptors)");
 
-    long long cap_grid = (long long)ctx->cus * wg_per_cu();
-    int grid = (int)(total_tiles < cap_grid ? total_tiles : cap_grid);
-    const int n = (int)need;
+    const MdqDesc *dd = reinterpret_cast<const MdqDesc *>(s.dev);
+    const int nd = (int)n;
+    const int grid = 0;   // one workgroup per tile (total_tiles)
     switch (storage) {
-    case mdq::ST_P4: e = mdq::launch_p4(s.dev, n, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream); break;
-    case mdq::ST_S8: e = mdq::launch_s8(s.dev, n, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream); break;
-    case mdq::ST_S16: e = mdq::launch_s16(s.dev, n, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream); break;
-    default: e = mdq::launch_s32(s.dev, n, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream); break;
+    case mdq::ST_P4: e = mdq::launch_p4(dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream); break;
+    case mdq::ST_S8: e = mdq::launch_s8(dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream); break;
+    case mdq::ST_S16: e = mdq::launch_s16(dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream); break;
+    default: e = mdq::launch_s32(dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream); break;
     }
     if (e != hipSuccess) return hip_fail(e, "kernel launch");
     e = hipEventRecord(s.done, stream);
@@ -322,6 +305,8 @@ int run(const stq_tensor *tensors, int n_tensors, int grad_dt, int ea_dt, int ea
         descs.push_back(d);
     }
     if (descs.empty()) return STQ_OK;
+    if (tiles > 0x7fffffffLL)
+        return fail(STQ_ERR_INVALID, "too many tiles in one call (%lld); split the tensor list", (long long)tiles);
     return upload_and_launch(descs, storage, grad_dt, log2b, rounding == STQ_ROUND_STOCHASTIC, tiles,
                              reinterpret_cast<unsigned long long *>(prof), seed,
                              reinterpret_cast<hipStream_t>(stream));

@@ -11,8 +11,11 @@ template <int ST, int GT, int LOG2B, bool SR>
 static hipError_t launch_one(const MdqDesc *d, int n, long long tiles, unsigned long long *prof,
                              unsigned long long seed, int grid, hipStream_t s)
 {
-    hipLaunchKernelGGL((mdq_step_kernel<ST, GT, LOG2B, SR>), dim3(grid), dim3(256), 0, s,
-                       d, n, tiles, prof, seed);
+    (void)grid;
+    // the compact tile_begin array follows the n descriptors in the same buffer
+    const long long *tb = reinterpret_cast<const long long *>(d + n);
+    hipLaunchKernelGGL((mdq_step_kernel<ST, GT, LOG2B, SR>), dim3((unsigned)tiles), dim3(256), 0, s,
+                       d, tb, n, prof, seed);
     return hipGetLastError();
 }
 

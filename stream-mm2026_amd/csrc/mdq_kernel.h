@@ -39,6 +39,27 @@ struct Cfg {
     static_assert(TB * B == TILE, "tile must hold whole blocks");
 };
 
+// Native vector types for the streaming accesses (the nontemporal builtins
+// take clang vector types, not HIP's struct vectors).
+typedef float vf4 __attribute__((ext_vector_type(4)));
+typedef uint32_t vu2 __attribute__((ext_vector_type(2)));
+typedef uint32_t vu4 __attribute__((ext_vector_type(4)));
+
+// Streaming (non-temporal) global accesses: every byte of p, g and the codes
+// is touched once per step, so they bypass cache allocation.
+// The tensor pointers come from the descriptor table, so the compiler cannot
+// infer their address space; casting to address space 1 (global) turns the
+// accesses into global_* instead of flat_* instructions.
+#define MDQ_GLOBAL __attribute__((address_space(1)))
+template <class T>
+__device__ __forceinline__ T ld_nt(const void *a) { return __builtin_nontemporal_load((const MDQ_GLOBAL T *)a); }
+template <class T>
+__device__ __forceinline__ void st_nt(T v, void *a) { __builtin_nontemporal_store(v, (MDQ_GLOBAL T *)a); }
+template <class T>
+__device__ __forceinline__ T ld_g(const void *a) { return *(const MDQ_GLOBAL T *)a; }
+template <class T>
+__device__ __forceinline__ void st_g(T v, void *a) { *(MDQ_GLOBAL T *)a = v; }
+
 // Offset inside the quant block of lane j's element e.
 template <int LOG2B>
 __device__ __forceinline__ int elem_off(int j, int e)
@@ -52,21 +73,21 @@ __device__ __forceinline__ int elem_off(int j, int e)
 template <int GT> struct GradIO;
 template <> struct GradIO<GT_F32> {
     static __device__ __forceinline__ void load4(const void *g, int64_t i, float *o) {
-        float4 v = *reinterpret_cast<const float4 *>(static_cast<const float *>(g) + i);
+        vf4 v = ld_nt<vf4>(static_cast<const float *>(g) + i);
         o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
     }
     static __device__ __forceinline__ float load1(const void *g, int64_t i) {
-        return static_cast<const float *>(g)[i];
+        return ld_g<float>(static_cast<const float *>(g) + i);
     }
 };
 template <> struct GradIO<GT_BF16> {
     static __device__ __forceinline__ void load4(const void *g, int64_t i, float *o) {
-        uint2 v = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(g) + i);
+        vu2 v = ld_nt<vu2>(static_cast<const uint16_t *>(g) + i);
         o[0] = bits_f(v.x << 16); o[1] = bits_f(v.x & 0xffff0000u);
         o[2] = bits_f(v.y << 16); o[3] = bits_f(v.y & 0xffff0000u);
     }
     static __device__ __forceinline__ float load1(const void *g, int64_t i) {
-        return bits_f((uint32_t)static_cast<const uint16_t *>(g)[i] << 16);
+        return bits_f((uint32_t)ld_g<uint16_t>(static_cast<const uint16_t *>(g) + i) << 16);
     }
 };
 template <> struct GradIO<GT_F16> {
@@ -74,12 +95,12 @@ template <> struct GradIO<GT_F16> {
         return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
     }
     static __device__ __forceinline__ void load4(const void *g, int64_t i, float *o) {
-        uint2 v = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(g) + i);
+        vu2 v = ld_nt<vu2>(static_cast<const uint16_t *>(g) + i);
         o[0] = h2f(v.x & 0xffffu); o[1] = h2f(v.x >> 16);
         o[2] = h2f(v.y & 0xffffu); o[3] = h2f(v.y >> 16);
     }
     static __device__ __forceinline__ float load1(const void *g, int64_t i) {
-        return h2f(static_cast<const uint16_t *>(g)[i]);
+        return h2f(ld_g<uint16_t>(static_cast<const uint16_t *>(g) + i));
     }
 };
 
@@ -89,7 +110,7 @@ template <> struct GradIO<GT_F16> {
 template <int ST> struct CodeIO;
 template <> struct CodeIO<ST_P4> {
     static __device__ __forceinline__ void load4(const MdqDesc &d, int64_t i, float *mc, uint32_t *vc) {
-        uint32_t w = *reinterpret_cast<const uint32_t *>(static_cast<const uint8_t *>(d.code_m) + i);
+        uint32_t w = ld_nt<uint32_t>(static_cast<const uint8_t *>(d.code_m) + i);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             uint32_t b = (w >> (8 * k)) & 0xffu;
@@ -98,7 +119,7 @@ template <> struct CodeIO<ST_P4> {
         }
     }
     static __device__ __forceinline__ void load1(const MdqDesc &d, int64_t i, float &mc, uint32_t &vc) {
-        uint32_t b = static_cast<const uint8_t *>(d.code_m)[i];
+        uint32_t b = ld_g<uint8_t>(static_cast<const uint8_t *>(d.code_m) + i);
         mc = (float)(b & 15u) - 8.0f;
         vc = b >> 4;
     }
@@ -108,16 +129,16 @@ template <> struct CodeIO<ST_P4> {
     static __device__ __forceinline__ void store4(const MdqDesc &d, int64_t i, const int32_t *qm, const uint32_t *qv) {
         uint32_t w = pack(qm[0], qv[0]) | (pack(qm[1], qv[1]) << 8) |
                      (pack(qm[2], qv[2]) << 16) | (pack(qm[3], qv[3]) << 24);
-        *reinterpret_cast<uint32_t *>(static_cast<uint8_t *>(d.code_m) + i) = w;
+        st_nt<uint32_t>(w, static_cast<uint8_t *>(d.code_m) + i);
     }
     static __device__ __forceinline__ void store1(const MdqDesc &d, int64_t i, int32_t qm, uint32_t qv) {
-        static_cast<uint8_t *>(d.code_m)[i] = (uint8_t)pack(qm, qv);
+        st_g<uint8_t>((uint8_t)pack(qm, qv), static_cast<uint8_t *>(d.code_m) + i);
     }
 };
 template <> struct CodeIO<ST_S8> {
     static __device__ __forceinline__ void load4(const MdqDesc &d, int64_t i, float *mc, uint32_t *vc) {
-        uint32_t wm = *reinterpret_cast<const uint32_t *>(static_cast<const int8_t *>(d.code_m) + i);
-        uint32_t wv = *reinterpret_cast<const uint32_t *>(static_cast<const uint8_t *>(d.code_v) + i);
+        uint32_t wm = ld_nt<uint32_t>(static_cast<const int8_t *>(d.code_m) + i);
+        uint32_t wv = ld_nt<uint32_t>(static_cast<const uint8_t *>(d.code_v) + i);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             mc[k] = (float)(int8_t)(wm >> (8 * k));
@@ -125,8 +146,8 @@ template <> struct CodeIO<ST_S8> {
         }
     }
     static __device__ __forceinline__ void load1(const MdqDesc &d, int64_t i, float &mc, uint32_t &vc) {
-        mc = (float)static_cast<const int8_t *>(d.code_m)[i];
-        vc = static_cast<const uint8_t *>(d.code_v)[i];
+        mc = (float)ld_g<int8_t>(static_cast<const int8_t *>(d.code_m) + i);
+        vc = ld_g<uint8_t>(static_cast<const uint8_t *>(d.code_v) + i);
     }
     static __device__ __forceinline__ void store4(const MdqDesc &d, int64_t i, const int32_t *qm, const uint32_t *qv) {
         uint32_t wm = 0, wv = 0;
@@ -135,58 +156,61 @@ template <> struct CodeIO<ST_S8> {
             wm |= ((uint32_t)qm[k] & 0xffu) << (8 * k);
             wv |= (qv[k] & 0xffu) << (8 * k);
         }
-        *reinterpret_cast<uint32_t *>(static_cast<int8_t *>(d.code_m) + i) = wm;
-        *reinterpret_cast<uint32_t *>(static_cast<uint8_t *>(d.code_v) + i) = wv;
+        st_nt<uint32_t>(wm, static_cast<int8_t *>(d.code_m) + i);
+        st_nt<uint32_t>(wv, static_cast<uint8_t *>(d.code_v) + i);
     }
     static __device__ __forceinline__ void store1(const MdqDesc &d, int64_t i, int32_t qm, uint32_t qv) {
-        static_cast<int8_t *>(d.code_m)[i] = (int8_t)qm;
-        static_cast<uint8_t *>(d.code_v)[i] = (uint8_t)qv;
+        st_g<int8_t>((int8_t)qm, static_cast<int8_t *>(d.code_m) + i);
+        st_g<uint8_t>((uint8_t)qv, static_cast<uint8_t *>(d.code_v) + i);
     }
 };
 template <> struct CodeIO<ST_S16> {
     static __device__ __forceinline__ void load4(const MdqDesc &d, int64_t i, float *mc, uint32_t *vc) {
-        uint2 wm = *reinterpret_cast<const uint2 *>(static_cast<const int16_t *>(d.code_m) + i);
-        uint2 wv = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(d.code_v) + i);
+        vu2 wm = ld_nt<vu2>(static_cast<const int16_t *>(d.code_m) + i);
+        vu2 wv = ld_nt<vu2>(static_cast<const uint16_t *>(d.code_v) + i);
         mc[0] = (float)(int16_t)wm.x; mc[1] = (float)(int16_t)(wm.x >> 16);
         mc[2] = (float)(int16_t)wm.y; mc[3] = (float)(int16_t)(wm.y >> 16);
         vc[0] = wv.x & 0xffffu; vc[1] = wv.x >> 16; vc[2] = wv.y & 0xffffu; vc[3] = wv.y >> 16;
     }
     static __device__ __forceinline__ void load1(const MdqDesc &d, int64_t i, float &mc, uint32_t &vc) {
-        mc = (float)static_cast<const int16_t *>(d.code_m)[i];
-        vc = static_cast<const uint16_t *>(d.code_v)[i];
+        mc = (float)ld_g<int16_t>(static_cast<const int16_t *>(d.code_m) + i);
+        vc = ld_g<uint16_t>(static_cast<const uint16_t *>(d.code_v) + i);
     }
     static __device__ __forceinline__ void store4(const MdqDesc &d, int64_t i, const int32_t *qm, const uint32_t *qv) {
-        uint2 wm, wv;
+        vu2 wm, wv;
         wm.x = ((uint32_t)qm[0] & 0xffffu) | ((uint32_t)qm[1] << 16);
         wm.y = ((uint32_t)qm[2] & 0xffffu) | ((uint32_t)qm[3] << 16);
         wv.x = (qv[0] & 0xffffu) | (qv[1] << 16);
         wv.y = (qv[2] & 0xffffu) | (qv[3] << 16);
-        *reinterpret_cast<uint2 *>(static_cast<int16_t *>(d.code_m) + i) = wm;
-        *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(d.code_v) + i) = wv;
+        st_nt<vu2>(wm, static_cast<int16_t *>(d.code_m) + i);
+        st_nt<vu2>(wv, static_cast<uint16_t *>(d.code_v) + i);
     }
     static __device__ __forceinline__ void store1(const MdqDesc &d, int64_t i, int32_t qm, uint32_t qv) {
-        static_cast<int16_t *>(d.code_m)[i] = (int16_t)qm;
-        static_cast<uint16_t *>(d.code_v)[i] = (uint16_t)qv;
+        st_g<int16_t>((int16_t)qm, static_cast<int16_t *>(d.code_m) + i);
+        st_g<uint16_t>((uint16_t)qv, static_cast<uint16_t *>(d.code_v) + i);
     }
 };
 template <> struct CodeIO<ST_S32> {
     static __device__ __forceinline__ void load4(const MdqDesc &d, int64_t i, float *mc, uint32_t *vc) {
-        int4 wm = *reinterpret_cast<const int4 *>(static_cast<const int32_t *>(d.code_m) + i);
-        uint4 wv = *reinterpret_cast<const uint4 *>(static_cast<const uint32_t *>(d.code_v) + i);
-        mc[0] = (float)wm.x; mc[1] = (float)wm.y; mc[2] = (float)wm.z; mc[3] = (float)wm.w;
+        vu4 wm = ld_nt<vu4>(static_cast<const int32_t *>(d.code_m) + i);
+        vu4 wv = ld_nt<vu4>(static_cast<const uint32_t *>(d.code_v) + i);
+        mc[0] = (float)(int32_t)wm.x; mc[1] = (float)(int32_t)wm.y;
+        mc[2] = (float)(int32_t)wm.z; mc[3] = (float)(int32_t)wm.w;
         vc[0] = wv.x; vc[1] = wv.y; vc[2] = wv.z; vc[3] = wv.w;
     }
     static __device__ __forceinline__ void load1(const MdqDesc &d, int64_t i, float &mc, uint32_t &vc) {
-        mc = (float)static_cast<const int32_t *>(d.code_m)[i];
-        vc = static_cast<const uint32_t *>(d.code_v)[i];
+        mc = (float)ld_g<int32_t>(static_cast<const int32_t *>(d.code_m) + i);
+        vc = ld_g<uint32_t>(static_cast<const uint32_t *>(d.code_v) + i);
     }
     static __device__ __forceinline__ void store4(const MdqDesc &d, int64_t i, const int32_t *qm, const uint32_t *qv) {
-        *reinterpret_cast<int4 *>(static_cast<int32_t *>(d.code_m) + i) = make_int4(qm[0], qm[1], qm[2], qm[3]);
-        *reinterpret_cast<uint4 *>(static_cast<uint32_t *>(d.code_v) + i) = make_uint4(qv[0], qv[1], qv[2], qv[3]);
+        vu4 wm = {(uint32_t)qm[0], (uint32_t)qm[1], (uint32_t)qm[2], (uint32_t)qm[3]};
+        vu4 wv = {qv[0], qv[1], qv[2], qv[3]};
+        st_nt<vu4>(wm, static_cast<int32_t *>(d.code_m) + i);
+        st_nt<vu4>(wv, static_cast<uint32_t *>(d.code_v) + i);
     }
     static __device__ __forceinline__ void store1(const MdqDesc &d, int64_t i, int32_t qm, uint32_t qv) {
-        static_cast<int32_t *>(d.code_m)[i] = qm;
-        static_cast<uint32_t *>(d.code_v)[i] = qv;
+        st_g<int32_t>(qm, static_cast<int32_t *>(d.code_m) + i);
+        st_g<uint32_t>(qv, static_cast<uint32_t *>(d.code_v) + i);
     }
 };
 
@@ -245,7 +269,11 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
 
     // old block scales (stquant_kernel.cu:67-69)
     float sm = 0.0f, sv = 0.0f, vmin = 0.0f;
-    if (blk_ok) { sm = d.scale_m[blk]; sv = d.scale_v[blk]; vmin = d.v_min[blk]; }
+    if (blk_ok) {
+        sm = ld_g<float>(d.scale_m + blk);
+        sv = ld_g<float>(d.scale_v + blk);
+        vmin = ld_g<float>(d.v_min + blk);
+    }
 
     float pv[EPL], gv[EPL], mc[EPL];
     uint32_t vc[EPL];
@@ -254,7 +282,7 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
 #pragma unroll
         for (int k = 0; k < C::QPL; ++k) {
             const int64_t i = base + 4 * (j + k * LPB);
-            float4 p4 = *reinterpret_cast<const float4 *>(d.p + i);
+            vf4 p4 = ld_nt<vf4>(d.p + i);
             pv[4 * k + 0] = p4.x; pv[4 * k + 1] = p4.y; pv[4 * k + 2] = p4.z; pv[4 * k + 3] = p4.w;
             GradIO<GT>::load4(d.g, i, gv + 4 * k);
             CodeIO<ST>::load4(d, i, mc + 4 * k, vc + 4 * k);
@@ -268,7 +296,7 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
             ok[e] = FULL || i < n;
             pv[e] = 0.0f; gv[e] = 0.0f; mc[e] = 0.0f; vc[e] = 0;
             if (ok[e]) {
-                pv[e] = d.p[i];
+                pv[e] = ld_g<float>(d.p + i);
                 gv[e] = GradIO<GT>::load1(d.g, i);
                 CodeIO<ST>::load1(d, i, mc[e], vc[e]);
             }
@@ -342,9 +370,9 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
     const float s_sv = ((lmax - lmin) + 1e-12f) / d.qvf;      // IEEE division
     const float s_vmin = lmin;
     if (j == 0 && blk_ok) {
-        d.scale_m[blk] = s_sm;
-        d.scale_v[blk] = s_sv;
-        d.v_min[blk] = s_vmin;
+        st_g<float>(s_sm, d.scale_m + blk);
+        st_g<float>(s_sv, d.scale_v + blk);
+        st_g<float>(s_vmin, d.v_min + blk);
     }
     if (prof_on) { unsigned long long t = clock64(); pa.c[2] += t - t0; t0 = t; }
 
@@ -438,8 +466,8 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
         for (int k = 0; k < C::QPL; ++k) {
             const int64_t i = base + 4 * (j + k * LPB);
             CodeIO<ST>::store4(d, i, qmi + 4 * k, qvi + 4 * k);
-            *reinterpret_cast<float4 *>(d.p + i) =
-                make_float4(pv[4 * k + 0], pv[4 * k + 1], pv[4 * k + 2], pv[4 * k + 3]);
+            vf4 o = {pv[4 * k + 0], pv[4 * k + 1], pv[4 * k + 2], pv[4 * k + 3]};
+            st_nt<vf4>(o, d.p + i);
         }
     } else {
 #pragma unroll
@@ -447,55 +475,47 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
             if (ok[e]) {
                 const int64_t i = base + elem_off<LOG2B>(j, e);
                 CodeIO<ST>::store1(d, i, qmi[e], qvi[e]);
-                d.p[i] = pv[e];
+                st_g<float>(pv[e], d.p + i);
             }
         }
     }
     if (prof_on) { unsigned long long t = clock64(); pa.c[4] += t - t0; }
 }
 
+// One workgroup per tile.  The tile's tensor is the largest t with
+// tile_begin[t] <= blockIdx.x (tile_begin: compact int64 copy of the
+// descriptors' tile starts, so the ~log2(n_desc) dependent scalar loads of the
+// search hit a few cache lines).  Profiling (prof != null) samples every 16th
+// workgroup; only the phase ratios of the cycle sums are meaningful.
 template <int ST, int GT, int LOG2B, bool SR>
-__global__ __launch_bounds__(256) void mdq_step_kernel(const MdqDesc *__restrict__ descs, int n_desc,
-                                                       long long total_tiles,
-                                                       unsigned long long *__restrict__ prof,
+__global__ __launch_bounds__(256) void mdq_step_kernel(const MdqDesc *__restrict__ descs,
+                                                       const long long *__restrict__ tile_begin,
+                                                       int n_desc, unsigned long long *__restrict__ prof,
                                                        unsigned long long seed)
 {
     using C = Cfg<LOG2B>;
     constexpr bool USE_LUT = (ST == ST_P4) && C::B >= 32;
-    __shared__ float lut_s[2][USE_LUT ? C::TB * 16 : 1];
-    __shared__ float xw_s[2][12];
+    __shared__ float lut_s[USE_LUT ? C::TB * 16 : 1];
+    __shared__ float xw_s[12];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-
-    long long tile = blockIdx.x;
-    if (tile >= total_tiles) return;
-    // first tensor: largest t with tile_begin <= tile
+    const long long tile = blockIdx.x;
     int lo = 0, hi = n_desc - 1;
     while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
-        if (descs[mid].tile_begin <= tile) lo = mid;
+        if (tile_begin[mid] <= tile) lo = mid;
         else hi = mid - 1;
     }
-    int ti = __builtin_amdgcn_readfirstlane(lo);
+    const MdqDesc &d = descs[__builtin_amdgcn_readfirstlane(lo)];
+    const long long tl = tile - d.tile_begin;
+    const bool prof_on = prof != nullptr && (blockIdx.x & 15) == 0;
     ProfAcc pa = {{0, 0, 0, 0, 0}};
-    const bool prof_on = prof != nullptr;
-    int parity = 0;
-    for (; tile < total_tiles; tile += gridDim.x) {
-        while (descs[ti].tile_end <= tile) ++ti;
-        const MdqDesc &d = descs[ti];
-        const long long tl = tile - d.tile_begin;
-        const bool full = (d.flags & DF_ALIGNED) && (tl + 1) * C::TILE <= d.numel;
-        float *lut = lut_s[parity];
-        float *xw = xw_s[parity];
-        if (full) mdq_step_tile<ST, GT, LOG2B, SR, true>(d, tl, lane, wave, lut, xw, seed, prof_on, pa);
-        else mdq_step_tile<ST, GT, LOG2B, SR, false>(d, tl, lane, wave, lut, xw, seed, prof_on, pa);
-        parity ^= 1;
-    }
-    if (prof_on) {
-        if (lane == 0) {
+    const bool full = (d.flags & DF_ALIGNED) && (tl + 1) * C::TILE <= d.numel;
+    if (full) mdq_step_tile<ST, GT, LOG2B, SR, true>(d, tl, lane, wave, lut_s, xw_s, seed, prof_on, pa);
+    else mdq_step_tile<ST, GT, LOG2B, SR, false>(d, tl, lane, wave, lut_s, xw_s, seed, prof_on, pa);
+    if (prof_on && threadIdx.x == 0) {
 #pragma unroll
-            for (int s = 0; s < 5; ++s) atomicAdd(prof + s, pa.c[s]);
-        }
+        for (int s = 0; s < 5; ++s) atomicAdd(prof + s, pa.c[s]);
     }
 }
 
