@@ -146,8 +146,8 @@ int stq_device_math_digests(int which, uint32_t first, uint32_t count, uint32_t 
 /* Host (CPU) builds of the same inline functions the kernels use. */
 void stq_host_math(int which, const float *x, float *y, int64_t n);
 /* out[i] = round-half-away(u[i] / d[i]) via the kernel's fp32 fma method,
- * with the reciprocal of d perturbed by inv_ulps units in the last place
- * (the device uses a hardware reciprocal within 1 ulp). */
+ * starting from the correctly rounded 1/d perturbed by inv_ulps units in the
+ * last place (the device starts from a hardware reciprocal within 1 ulp). */
 void stq_host_round_half_away(const float *u, const float *d, float *out, int64_t n, int inv_ulps);
 void stq_host_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
 

@@ -91,8 +91,6 @@ int storage_width(int st)
 
 int code_bytes(int st) { return st == mdq::ST_P4 ? 1 : storage_width(st) / 8; }
 
-// Elements per tile for a block size (see Cfg in mdq_kernel.h).
-int64_t tile_elems(int B) { return 256 * (B >= 8 ? 8 : B); }
 
 bool is_aligned(const void *ptr, int bytes) { return ((uintptr_t)ptr % (uintptr_t)bytes) == 0; }
 
@@ -280,7 +278,7 @@ int run(const stq_tensor *tensors, int n_tensors, int grad_dt, int ea_dt, int ea
     if (rc != STQ_OK) return rc;
     if (n_tensors < 0 || (n_tensors > 0 && !tensors)) return fail(STQ_ERR_INVALID, "bad tensor list");
     const int B = 1 << log2b;
-    const int64_t te = tile_elems(B);
+    const int64_t te = mdq::tile_elems(B);
     std::vector<MdqDesc> descs;
     descs.reserve((size_t)n_tensors);
     int storage = -1;
@@ -397,7 +395,7 @@ void stq_host_round_half_away(const float *u, const float *d, float *out, int64_
 {
     for (int64_t i = 0; i < n; ++i) {
         const float inv = mdq::bits_f(mdq::f_bits(1.0f / d[i]) + (uint32_t)inv_ulps);
-        out[i] = mdq::mdq_round_half_away(u[i], d[i], inv, 0.5f * d[i]);
+        out[i] = mdq::mdq_round_half_away(u[i], d[i], mdq::mdq_inv_lo(inv), 0.5f * d[i]);
     }
 }
 

@@ -43,4 +43,11 @@ struct alignas(16) MdqDesc {
 
 static_assert(sizeof(MdqDesc) % 16 == 0, "descriptor must stay 16-byte sized");
 
+// Tile geometry shared by the host launcher and the kernel: a quant block of
+// B elements is owned by B/EPL lanes (EPL = min(B, 8) elements per lane); a
+// workgroup is one wave, or two for B = 1024, and one tile is one workgroup.
+constexpr int tile_epl(int B) { return B >= 8 ? 8 : B; }
+constexpr int tile_threads(int B) { return B / tile_epl(B) > 64 ? 2 * 64 : 64; }
+constexpr int tile_elems(int B) { return tile_threads(B) * tile_epl(B); }
+
 }  // namespace mdq

@@ -14,8 +14,8 @@ static hipError_t launch_one(const MdqDesc *d, int n, long long tiles, unsigned 
     (void)grid;
     // the compact tile_begin array follows the n descriptors in the same buffer
     const long long *tb = reinterpret_cast<const long long *>(d + n);
-    hipLaunchKernelGGL((mdq_step_kernel<ST, GT, LOG2B, SR>), dim3((unsigned)tiles), dim3(256), 0, s,
-                       d, tb, n, prof, seed);
+    hipLaunchKernelGGL((mdq_step_kernel<ST, GT, LOG2B, SR>), dim3((unsigned)tiles),
+                       dim3(Cfg<LOG2B>::THREADS), 0, s, d, tb, n, prof, seed);
     return hipGetLastError();
 }
 

@@ -33,10 +33,13 @@ struct Cfg {
     static constexpr int EPL = B >= 8 ? 8 : B;            // elements per lane
     static constexpr int LPB = B / EPL;                    // lanes per quant block
     static constexpr int QPL = EPL >= 4 ? EPL / 4 : 0;     // 4-element quads per lane
-    static constexpr int TB = LPB <= 64 ? 256 / LPB : 2;   // quant blocks per tile
-    static constexpr int BPW = LPB <= 64 ? 64 / LPB : 0;   // quant blocks per wave
-    static constexpr int TILE = 256 * EPL;                 // elements per tile
+    static constexpr int WAVES = LPB > 64 ? LPB / 64 : 1;  // waves per workgroup (tile)
+    static constexpr int THREADS = 64 * WAVES;
+    static constexpr int TILE = THREADS * EPL;             // elements per tile
+    static constexpr int TB = TILE / B;                    // quant blocks per tile
     static_assert(TB * B == TILE, "tile must hold whole blocks");
+    static_assert(EPL == tile_epl(B) && THREADS == tile_threads(B) && TILE == tile_elems(B),
+                  "kernel tile geometry must match the host launcher's");
 };
 
 // Native vector types for the streaming accesses (the nontemporal builtins
@@ -105,23 +108,34 @@ template <> struct GradIO<GT_F16> {
 };
 
 // ---------------------------------------------------------------- code I/O
-// mc: the m code as float, already minus 8 for packed nibbles (the value the
-// reference multiplies by scale_m); vc: the raw v code.
+// mc: the m code as float (for packed nibbles the stored nibble q + 8, which
+// dequant_m offsets by 8); vc: the raw v code.
 template <int ST> struct CodeIO;
 template <> struct CodeIO<ST_P4> {
     static __device__ __forceinline__ void load4(const MdqDesc &d, int64_t i, float *mc, uint32_t *vc) {
-        uint32_t w = ld_nt<uint32_t>(static_cast<const uint8_t *>(d.code_m) + i);
+        const uint32_t w = ld_nt<uint32_t>(static_cast<const uint8_t *>(d.code_m) + i);
+        const uint32_t lo = w & 0x0f0f0f0fu;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            uint32_t b = (w >> (8 * k)) & 0xffu;
-            mc[k] = (float)(b & 15u) - 8.0f;
-            vc[k] = b >> 4;
+            mc[k] = (float)((lo >> (8 * k)) & 0xffu);
+            vc[k] = (w >> (8 * k + 4)) & 15u;
         }
     }
     static __device__ __forceinline__ void load1(const MdqDesc &d, int64_t i, float &mc, uint32_t &vc) {
         uint32_t b = ld_g<uint8_t>(static_cast<const uint8_t *>(d.code_m) + i);
-        mc = (float)(b & 15u) - 8.0f;
+        mc = (float)(b & 15u);
         vc = b >> 4;
+    }
+    // byte values already formed as floats (exact integers 0..255)
+    static __device__ __forceinline__ void store4f(const MdqDesc &d, int64_t i, const float *pk) {
+        uint32_t w = __builtin_amdgcn_cvt_pk_u8_f32(pk[0], 0, 0u);
+        w = __builtin_amdgcn_cvt_pk_u8_f32(pk[1], 1, w);
+        w = __builtin_amdgcn_cvt_pk_u8_f32(pk[2], 2, w);
+        w = __builtin_amdgcn_cvt_pk_u8_f32(pk[3], 3, w);
+        st_nt<uint32_t>(w, static_cast<uint8_t *>(d.code_m) + i);
+    }
+    static __device__ __forceinline__ void store1f(const MdqDesc &d, int64_t i, float pk) {
+        st_g<uint8_t>((uint8_t)(uint32_t)pk, static_cast<uint8_t *>(d.code_m) + i);
     }
     static __device__ __forceinline__ uint32_t pack(int32_t qm, uint32_t qv) {
         return (qv << 4) | (uint32_t)(qm + 8);
@@ -215,27 +229,34 @@ template <> struct CodeIO<ST_S32> {
 };
 
 // ------------------------------------------------------- cross-lane reduction
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float x)
+// Block reductions run on integer keys: |m| >= 0 orders like its bit pattern,
+// and log v maps to a signed key that orders like the float (negative values
+// get their magnitude bits flipped).  Integer max/min need no NaN
+// canonicalisation, so the DPP row operations fold into them.
+__device__ __forceinline__ int32_t f2key(float x)
 {
-    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xF, 0xF, true));
+    const int32_t b = __builtin_bit_cast(int32_t, x);
+    return b ^ ((b >> 31) & 0x7fffffff);
 }
+__device__ __forceinline__ float key2f(int32_t k) { return __builtin_bit_cast(float, k ^ ((k >> 31) & 0x7fffffff)); }
+
+template <int CTRL>
+__device__ __forceinline__ int32_t dpp_i(int32_t x) { return __builtin_amdgcn_mov_dpp(x, CTRL, 0xF, 0xF, true); }
 
 template <bool IS_MAX>
-__device__ __forceinline__ float op_(float a, float b) { return IS_MAX ? fmaxf(a, b) : fminf(a, b); }
+__device__ __forceinline__ int32_t iop(int32_t a, int32_t b) { return IS_MAX ? (a > b ? a : b) : (a < b ? a : b); }
 
 // Reduce over aligned groups of LANES lanes (LANES <= 64); every lane of the
 // group receives the result.
 template <int LANES, bool IS_MAX>
-__device__ __forceinline__ float group_reduce(float x)
+__device__ __forceinline__ int32_t group_reduce(int32_t x)
 {
-    if constexpr (LANES >= 2) x = op_<IS_MAX>(x, dpp_f<0xB1>(x));   // quad_perm [1,0,3,2]
-    if constexpr (LANES >= 4) x = op_<IS_MAX>(x, dpp_f<0x4E>(x));   // quad_perm [2,3,0,1]
-    if constexpr (LANES >= 8) x = op_<IS_MAX>(x, dpp_f<0x141>(x));  // row_half_mirror
-    if constexpr (LANES >= 16) x = op_<IS_MAX>(x, dpp_f<0x140>(x)); // row_mirror
-    if constexpr (LANES >= 32)                                      // lane ^ 16 within 32
-        x = op_<IS_MAX>(x, __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), 0x401F)));
-    if constexpr (LANES >= 64) x = op_<IS_MAX>(x, __shfl_xor(x, 32));
+    if constexpr (LANES >= 2) x = iop<IS_MAX>(x, dpp_i<0xB1>(x));   // quad_perm [1,0,3,2]
+    if constexpr (LANES >= 4) x = iop<IS_MAX>(x, dpp_i<0x4E>(x));   // quad_perm [2,3,0,1]
+    if constexpr (LANES >= 8) x = iop<IS_MAX>(x, dpp_i<0x141>(x));  // row_half_mirror
+    if constexpr (LANES >= 16) x = iop<IS_MAX>(x, dpp_i<0x140>(x)); // row_mirror
+    if constexpr (LANES >= 32) x = iop<IS_MAX>(x, __builtin_amdgcn_ds_swizzle(x, 0x401F));  // lane ^ 16
+    if constexpr (LANES >= 64) x = iop<IS_MAX>(x, __shfl_xor(x, 32));
     return x;
 }
 
@@ -243,13 +264,23 @@ struct ProfAcc {
     unsigned long long c[5];
 };
 
+// Dequantised m from its stored code.  Packed nibbles hold mu = q + 8;
+// ((float)mu - 8) * sm == fma(mu, sm, -8 * sm) exactly (one rounding of the
+// same real number; -8*sm is exact), up to the sign of a zero product.
+template <int ST>
+__device__ __forceinline__ float dequant_m(float code, float sm, float neg8sm)
+{
+    if constexpr (ST == ST_P4) return fma_(code, sm, neg8sm);
+    else return code * sm;
+}
+
 // ---------------------------------------------------------------- one tile
 // FULL: every element of the tile lies inside the tensor and all pointers are
 // 16-byte aligned, so vector accesses are used; otherwise every access is
 // guarded by idx < numel.
 template <int ST, int GT, int LOG2B, bool SR, bool FULL>
 __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int lane, int wave,
-                                              float *lut, float *xw, unsigned long long seed,
+                                              float *lut, int32_t *xw, unsigned long long seed,
                                               bool prof_on, ProfAcc &pa)
 {
     using C = Cfg<LOG2B>;
@@ -260,8 +291,8 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
     if (prof_on) t0 = clock64();
 
     int bi, j;
-    if constexpr (LPB <= 64) { bi = wave * C::BPW + lane / LPB; j = lane % LPB; }
-    else { bi = wave >> 1; j = ((wave & 1) << 6) | lane; }
+    if constexpr (LPB <= 64) { bi = lane / LPB; j = lane % LPB; }
+    else { bi = 0; j = (wave << 6) | lane; }
     const int64_t n = d.numel;
     const int64_t blk = tl * C::TB + bi;
     const int64_t base = blk << LOG2B;
@@ -313,7 +344,7 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
                 if (e < 16) tab[e] = mdq_expf(fma_((float)e, sv, vmin));
             }
         }
-        if constexpr (LPB <= 64) {
+        if constexpr (C::WAVES == 1) {
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -325,10 +356,11 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
 
     // dequant + AdamW moments (stquant_kernel.cu:71-85); contraction fixed as
     // one fma for the v exponent and one for each moment.
+    const float neg8sm = -8.0f * sm;
     float m[EPL], v[EPL], lv[EPL];
 #pragma unroll
     for (int e = 0; e < EPL; ++e) {
-        const float m0 = mc[e] * sm;
+        const float m0 = dequant_m<ST>(mc[e], sm, neg8sm);
         float v0;
         if constexpr (USE_LUT) v0 = lut[bi * 16 + vc[e]];
         else v0 = mdq_expf(fma_((float)vc[e], sv, vmin));
@@ -340,7 +372,7 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
 
     // |m|, log(v + 1e-12) and the three block reductions (:92-97); lanes
     // outside the tensor contribute 0 to all three.
-    float amax, lmax, lmin;
+    float amax = 0.0f, lmax = 0.0f, lmin = 0.0f;
 #pragma unroll
     for (int e = 0; e < EPL; ++e) {
         const float a = ok[e] ? fabsf(m[e]) : 0.0f;
@@ -349,21 +381,25 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
         if (e == 0) { amax = a; lmax = l; lmin = l; }
         else { amax = fmaxf(amax, a); lmax = fmaxf(lmax, l); lmin = fminf(lmin, l); }
     }
+    int32_t ka = __builtin_bit_cast(int32_t, amax), kx = f2key(lmax), kn = f2key(lmin);
     if constexpr (LPB <= 64) {
-        amax = group_reduce<LPB, true>(amax);
-        lmax = group_reduce<LPB, true>(lmax);
-        lmin = group_reduce<LPB, false>(lmin);
+        ka = group_reduce<LPB, true>(ka);
+        kx = group_reduce<LPB, true>(kx);
+        kn = group_reduce<LPB, false>(kn);
     } else {
-        amax = group_reduce<64, true>(amax);
-        lmax = group_reduce<64, true>(lmax);
-        lmin = group_reduce<64, false>(lmin);
-        if (lane == 0) { xw[wave * 3 + 0] = amax; xw[wave * 3 + 1] = lmax; xw[wave * 3 + 2] = lmin; }
+        ka = group_reduce<64, true>(ka);
+        kx = group_reduce<64, true>(kx);
+        kn = group_reduce<64, false>(kn);
+        if (lane == 0) { xw[wave * 3 + 0] = ka; xw[wave * 3 + 1] = kx; xw[wave * 3 + 2] = kn; }
         __syncthreads();
         const int o = (wave ^ 1) * 3;
-        amax = fmaxf(amax, xw[o + 0]);
-        lmax = fmaxf(lmax, xw[o + 1]);
-        lmin = fminf(lmin, xw[o + 2]);
+        ka = iop<true>(ka, xw[o + 0]);
+        kx = iop<true>(kx, xw[o + 1]);
+        kn = iop<false>(kn, xw[o + 2]);
     }
+    amax = __builtin_bit_cast(float, ka);
+    lmax = key2f(kx);
+    lmin = key2f(kn);
 
     // new scales (:101-106)
     const float s_sm = (amax + 1e-12f) * d.inv_qm;            // == / 2^(bits-1), exact
@@ -378,16 +414,15 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
 
     // requant (:112-131)
     const float dm = s_sm + 1e-12f, dv = s_sv + 1e-12f;
-    const float hdm = 0.5f * dm, hdv = 0.5f * dv;
     int32_t qmi[EPL];
     uint32_t qvi[EPL];
+    float pk[EPL];                                            // packed byte values (P4)
     const bool wide = (ST == ST_S32) && d.bits > 16;          // uniform per tensor
     if (!wide) {
-        float inv_dm, inv_dv;
-        if constexpr (SR) { inv_dm = 1.0f / dm; inv_dv = 1.0f / dv; }
-        else { inv_dm = __builtin_amdgcn_rcpf(dm); inv_dv = __builtin_amdgcn_rcpf(dv); }
-        float um[EPL], uv[EPL];
+        float qmf[EPL], qvf[EPL];
         if constexpr (SR) {
+            const float inv_dm = 1.0f / dm, inv_dv = 1.0f / dv;
+            float um[EPL], uv[EPL];
             // Philox4x32-10 per 4-element quad of the tensor: counter
             // (quad index lo, hi, tensor id, step), key = seed; word i of the
             // output serves element 4q+i (low half -> m, high half -> v).
@@ -417,23 +452,32 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
                     uv[e] = mdq_u16_uniform(ww >> 16);
                 }
             }
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) {
+                qmf[e] = floor_(fma_(m[e], inv_dm, um[e]));
+                qvf[e] = floor_(fma_(lv[e] - s_vmin, inv_dv, uv[e]));
+            }
+        } else {
+            const float hdm = 0.5f * dm, hdv = 0.5f * dv;
+            const float ilm = mdq_inv_lo(__builtin_amdgcn_rcpf(dm));
+            const float ilv = mdq_inv_lo(__builtin_amdgcn_rcpf(dv));
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) {
+                const float K = mdq_round_half_away(fabsf(m[e]), dm, ilm, hdm);
+                qmf[e] = __builtin_copysignf(K, m[e]);
+                qvf[e] = mdq_round_half_away(lv[e] - s_vmin, dv, ilv, hdv);
+            }
         }
 #pragma unroll
         for (int e = 0; e < EPL; ++e) {
-            float qmf, qvf;
-            const float u = lv[e] - s_vmin;
-            if constexpr (SR) {
-                qmf = floor_(fma_(m[e], inv_dm, um[e]));
-                qvf = floor_(fma_(u, inv_dv, uv[e]));
+            const float qm = __builtin_amdgcn_fmed3f(qmf[e], -d.qm, d.qm - 1.0f);
+            const float qv = __builtin_amdgcn_fmed3f(qvf[e], 0.0f, d.qv);
+            if constexpr (ST == ST_P4) {
+                pk[e] = fma_(qv, 16.0f, qm + 8.0f);           // (v << 4) | (m + 8), exact
             } else {
-                const float K = mdq_round_half_away(fabsf(m[e]), dm, inv_dm, hdm);
-                qmf = m[e] < 0.0f ? -K : K;
-                qvf = mdq_round_half_away(u, dv, inv_dv, hdv);
+                qmi[e] = (int32_t)qm;
+                qvi[e] = (uint32_t)(int32_t)qv;
             }
-            qmf = fminf(fmaxf(qmf, -d.qm), d.qm - 1.0f);
-            qvf = fminf(fmaxf(qvf, 0.0f), d.qv);
-            qmi[e] = (int32_t)qmf;
-            qvi[e] = (uint32_t)(int32_t)qvf;
         }
     } else {
         // 17..32-bit codes: the reference's FP64 path verbatim.
@@ -465,7 +509,8 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
 #pragma unroll
         for (int k = 0; k < C::QPL; ++k) {
             const int64_t i = base + 4 * (j + k * LPB);
-            CodeIO<ST>::store4(d, i, qmi + 4 * k, qvi + 4 * k);
+            if constexpr (ST == ST_P4) CodeIO<ST>::store4f(d, i, pk + 4 * k);
+            else CodeIO<ST>::store4(d, i, qmi + 4 * k, qvi + 4 * k);
             vf4 o = {pv[4 * k + 0], pv[4 * k + 1], pv[4 * k + 2], pv[4 * k + 3]};
             st_nt<vf4>(o, d.p + i);
         }
@@ -474,7 +519,8 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
         for (int e = 0; e < EPL; ++e) {
             if (ok[e]) {
                 const int64_t i = base + elem_off<LOG2B>(j, e);
-                CodeIO<ST>::store1(d, i, qmi[e], qvi[e]);
+                if constexpr (ST == ST_P4) CodeIO<ST>::store1f(d, i, pk[e]);
+                else CodeIO<ST>::store1(d, i, qmi[e], qvi[e]);
                 st_g<float>(pv[e], d.p + i);
             }
         }
@@ -482,24 +528,30 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
     if (prof_on) { unsigned long long t = clock64(); pa.c[4] += t - t0; }
 }
 
-// One workgroup per tile.  The tile's tensor is the largest t with
-// tile_begin[t] <= blockIdx.x (tile_begin: compact int64 copy of the
-// descriptors' tile starts, so the ~log2(n_desc) dependent scalar loads of the
-// search hit a few cache lines).  Profiling (prof != null) samples every 16th
-// workgroup; only the phase ratios of the cycle sums are meaningful.
+// One workgroup per tile.  Workgroup b runs on XCD b % 8 (the hardware's
+// round-robin); it takes tile x*q + min(x, r) + b/8 (x = b % 8, q, r = grid
+// / 8, grid % 8), so each XCD streams one contiguous eighth of the tensors
+// (a bijection on [0, grid)).  The tile's tensor is the largest t with
+// tile_begin[t] <= tile (tile_begin: compact int64 copy of the descriptors'
+// tile starts, so the ~log2(n_desc) dependent scalar loads hit a few cache
+// lines).  Profiling (prof != null) samples every 64th tile; only the phase
+// ratios of the cycle sums are meaningful.
 template <int ST, int GT, int LOG2B, bool SR>
-__global__ __launch_bounds__(256) void mdq_step_kernel(const MdqDesc *__restrict__ descs,
-                                                       const long long *__restrict__ tile_begin,
-                                                       int n_desc, unsigned long long *__restrict__ prof,
-                                                       unsigned long long seed)
+__global__ __launch_bounds__(Cfg<LOG2B>::THREADS) void mdq_step_kernel(const MdqDesc *__restrict__ descs,
+                                                                      const long long *__restrict__ tile_begin,
+                                                                      int n_desc,
+                                                                      unsigned long long *__restrict__ prof,
+                                                                      unsigned long long seed)
 {
     using C = Cfg<LOG2B>;
     constexpr bool USE_LUT = (ST == ST_P4) && C::B >= 32;
     __shared__ float lut_s[USE_LUT ? C::TB * 16 : 1];
-    __shared__ float xw_s[12];
+    __shared__ int32_t xw_s[6];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const long long tile = blockIdx.x;
+    const unsigned grid = gridDim.x, b = blockIdx.x;
+    const unsigned q = grid >> 3, r = grid & 7u, x = b & 7u;
+    const long long tile = (long long)x * q + (x < r ? x : r) + (b >> 3);
     int lo = 0, hi = n_desc - 1;
     while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
@@ -508,7 +560,7 @@ __global__ __launch_bounds__(256) void mdq_step_kernel(const MdqDesc *__restrict
     }
     const MdqDesc &d = descs[__builtin_amdgcn_readfirstlane(lo)];
     const long long tl = tile - d.tile_begin;
-    const bool prof_on = prof != nullptr && (blockIdx.x & 15) == 0;
+    const bool prof_on = prof != nullptr && (tile & 63) == 0;
     ProfAcc pa = {{0, 0, 0, 0, 0}};
     const bool full = (d.flags & DF_ALIGNED) && (tl + 1) * C::TILE <= d.numel;
     if (full) mdq_step_tile<ST, GT, LOG2B, SR, true>(d, tl, lane, wave, lut_s, xw_s, seed, prof_on, pa);

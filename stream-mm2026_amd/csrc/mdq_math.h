@@ -13,7 +13,7 @@
 //   caller gets the same bits on any IEEE-conforming target.
 // * mdq_round_half_away: round(u / d) for u >= 0 with ties away from zero,
 //   exactly as round((double)u / (double)d) (stquant_kernel.cu:113,123)
-//   evaluates for quotients below 2^17, using fp32 fma residuals only.
+//   evaluates for quotients below 2^19, using one fp32 fma residual.
 // * mdq_philox4x32_10: Philox4x32-10 (Salmon et al., SC'11).
 #pragma once
 #include <stdint.h>
@@ -99,20 +99,23 @@ MDQ_HD float mdq_logf(float x)
 }
 
 // K = floor(u/d + 1/2) for u >= 0 and d a positive normal float, i.e.
-// round-half-away(u/d).  Exact whenever the candidate k0 = floor(u*inv_d + .5)
-// is within one of u/d, which holds for u/d < 2^17 and inv_d within 2 ulp of
-// 1/d.  Then R = u - k0*d is exactly representable (u >= d/2 puts u and k0*d
-// on a common 2^(E_d-24) grid, |R| <= d), and the decisions R >= d/2 and
-// R < -d/2 are exact; u < d/2 always rounds to 0.  hd must be d/2 exactly.
-MDQ_HD float mdq_round_half_away(float u, float d, float inv_d, float hd)
+// round-half-away(u/d), computed exactly in fp32 as long as u/d < 2^19.
+// inv_lo must lie below 1/d by a relative 2^-23 .. 2^-20 (the kernel takes
+// the hardware reciprocal, within 1 ulp, and steps it down 4 ulp).  Then the
+// candidate k0 = floor(u*inv_lo + 1/2) is K or K-1, never above K, and
+// R = u - k0*d (one fma) decides: K = k0 + (R >= d/2).  R is exact when
+// u >= d/2 (u and k0*d share the 2^(E_d-24) grid and |R| < 2^(E_d)), or else
+// |R| >= 2^(E_d) > d/2 and only its sign matters; when u < d/2, k0 = 0 and R = u.
+// hd must be d/2 exactly.
+MDQ_HD float mdq_round_half_away(float u, float d, float inv_lo, float hd)
 {
-    float k0 = floor_(fma_(u, inv_d, 0.5f));
-    float R = fma_(-k0, d, u);
-    float K = k0;
-    K = (R >= hd) ? K + 1.0f : K;
-    K = (R < -hd) ? K - 1.0f : K;
-    return (u < hd) ? 0.0f : K;
+    const float k0 = floor_(fma_(u, inv_lo, 0.5f));
+    const float R = fma_(-k0, d, u);
+    return R >= hd ? k0 + 1.0f : k0;
 }
+
+// The reciprocal of d stepped down by 4 ulp, for mdq_round_half_away.
+MDQ_HD float mdq_inv_lo(float inv_d_within_1ulp) { return bits_f(f_bits(inv_d_within_1ulp) - 4u); }
 
 struct U4 { uint32_t x, y, z, w; };
 

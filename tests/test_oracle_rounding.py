@@ -52,7 +52,7 @@ def test_oracle_round_div_is_half_away():
     assert orc.round_div(0.5, 1.0) == 1.0 and orc.round_div(-0.5, 1.0) == -1.0
 
 
-@pytest.mark.parametrize("inv_ulps", [-2, -1, 0, 1, 2])
+@pytest.mark.parametrize("inv_ulps", [-1, 0, 1])
 def test_fp32_method_equals_fp64_round(inv_ulps):
     rng = np.random.default_rng(100 + inv_ulps)
     u1, d1 = _cases(rng, 400_000)
@@ -79,5 +79,5 @@ def test_fp32_method_small_brute_force():
         u = np.concatenate([u, np.nextafter(u, np.float32(np.inf)), np.nextafter(u, np.float32(0))])
         dd = np.full_like(u, d)
         ref = round_half_away_f64(u.astype(np.float64) / dd.astype(np.float64))
-        for inv in (-2, 0, 2):
+        for inv in (-1, 0, 1):
             assert np.array_equal(mdq_hip.host_round_half_away(u, dd, inv), ref)
