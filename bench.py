@@ -59,9 +59,15 @@ def gpt2_small_shapes():
     return shapes
 
 
+def llama7b_flat_shapes():
+    """The LLaMA-7B parameter count as one flat tensor (isolates per-tensor overheads)."""
+    return [("flat", sum(n for _, n in llama7b_shapes()))]
+
+
 CONFIGS = {
     # name: (shapes, grad dtype, bits, block)
     "llama7b": (llama7b_shapes, "bf16", 4, 128),
+    "llama7b_flat": (llama7b_flat_shapes, "bf16", 4, 128),
     "gpt2": (gpt2_small_shapes, "f32", 4, 128),
 }
 

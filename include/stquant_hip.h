@@ -149,6 +149,9 @@ void stq_host_math(int which, const float *x, float *y, int64_t n);
  * starting from the correctly rounded 1/d perturbed by inv_ulps units in the
  * last place (the device starts from a hardware reciprocal within 1 ulp). */
 void stq_host_round_half_away(const float *u, const float *d, float *out, int64_t n, int inv_ulps);
+/* out[i] = x[i] / (2^bits - 1) as the kernel computes the new v scale
+ * (a correction step that must equal IEEE division). */
+void stq_host_div_code_range(const float *x, float *out, int64_t n, int bits);
 void stq_host_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
 
 #ifdef __cplusplus

@@ -143,7 +143,7 @@ int make_desc(const stq_tensor &t, int storage, int grad_dt, int B, MdqDesc &d)
     d.qm = ldexpf(1.0f, t.bits - 1);
     d.inv_qm = ldexpf(1.0f, -(t.bits - 1));
     d.qvf = (float)(std::ldexp(1.0, t.bits) - 1.0);
-    d.qv = d.qvf;
+    d.inv_qvf = 1.0f / d.qvf;
     d.bits = (uint32_t)t.bits;
     d.step = (uint32_t)t.step;
     d.tensor_id = t.tensor_id;
@@ -397,6 +397,13 @@ void stq_host_round_half_away(const float *u, const float *d, float *out, int64_
         const float inv = mdq::bits_f(mdq::f_bits(1.0f / d[i]) + (uint32_t)inv_ulps);
         out[i] = mdq::mdq_round_half_away(u[i], d[i], mdq::mdq_inv_lo(inv), 0.5f * d[i]);
     }
+}
+
+void stq_host_div_code_range(const float *x, float *out, int64_t n, int bits)
+{
+    const float D = (float)(std::ldexp(1.0, bits) - 1.0);
+    const float y = 1.0f / D;
+    for (int64_t i = 0; i < n; ++i) out[i] = mdq::mdq_div_code_range(x[i], D, y);
 }
 
 void stq_host_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4])

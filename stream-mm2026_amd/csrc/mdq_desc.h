@@ -33,8 +33,9 @@ struct alignas(16) MdqDesc {
     float step_size;      // lr / (1 - beta1^t)
     float inv_sqrt_bc2;   // 1 / sqrt(1 - beta2^t)
     float decay;          // 1 - lr * weight_decay (1 when weight_decay == 0)
-    // Code range: m in [-qm, qm - 1], v in [0, qv]; inv_qm = 1 / qm (a power of two).
-    float qm, qv, inv_qm, qvf;  // qvf = (float)(2^bits - 1) as the reference divides by it
+    // Code range: m in [-qm, qm - 1], v in [0, qvf]; inv_qm = 1 / qm (a power of
+    // two); qvf = (float)(2^bits - 1), the reference's divisor, inv_qvf = RN(1 / qvf).
+    float qm, inv_qvf, inv_qm, qvf;
     uint32_t bits;
     uint32_t step;
     uint32_t tensor_id;

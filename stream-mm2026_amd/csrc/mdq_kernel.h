@@ -264,6 +264,20 @@ struct ProfAcc {
     unsigned long long c[5];
 };
 
+// The descriptor with its element pointers advanced to element `off`
+// (workgroup-uniform, so the copies live in scalar registers).
+template <int ST, int GT>
+__device__ __forceinline__ MdqDesc tile_view(const MdqDesc &d, int64_t off)
+{
+    MdqDesc t = d;
+    t.p = d.p + off;
+    t.g = static_cast<const char *>(d.g) + off * (GT == GT_F32 ? 4 : 2);
+    constexpr int cb = ST == ST_P4 ? 1 : ST == ST_S8 ? 1 : ST == ST_S16 ? 2 : 4;
+    t.code_m = static_cast<char *>(d.code_m) + off * cb;
+    if constexpr (ST != ST_P4) t.code_v = static_cast<char *>(d.code_v) + off * cb;
+    return t;
+}
+
 // Dequantised m from its stored code.  Packed nibbles hold mu = q + 8;
 // ((float)mu - 8) * sm == fma(mu, sm, -8 * sm) exactly (one rounding of the
 // same real number; -8*sm is exact), up to the sign of a zero product.
@@ -309,14 +323,20 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
     float pv[EPL], gv[EPL], mc[EPL];
     uint32_t vc[EPL];
     bool ok[EPL];
+    // FULL tiles address through a workgroup-uniform tile base (scalar
+    // registers) plus a 32-bit lane offset, so loads and stores take the
+    // saddr + voffset form instead of 64-bit per-lane address arithmetic.
+    const int64_t tbase = tl * C::TILE;
+    const uint32_t lbase = (uint32_t)bi * B;
     if constexpr (FULL && C::QPL > 0) {
+        const MdqDesc dt = tile_view<ST, GT>(d, tbase);
 #pragma unroll
         for (int k = 0; k < C::QPL; ++k) {
-            const int64_t i = base + 4 * (j + k * LPB);
-            vf4 p4 = ld_nt<vf4>(d.p + i);
+            const uint32_t i = lbase + 4 * (j + k * LPB);
+            vf4 p4 = ld_nt<vf4>(dt.p + i);
             pv[4 * k + 0] = p4.x; pv[4 * k + 1] = p4.y; pv[4 * k + 2] = p4.z; pv[4 * k + 3] = p4.w;
-            GradIO<GT>::load4(d.g, i, gv + 4 * k);
-            CodeIO<ST>::load4(d, i, mc + 4 * k, vc + 4 * k);
+            GradIO<GT>::load4(dt.g, i, gv + 4 * k);
+            CodeIO<ST>::load4(dt, i, mc + 4 * k, vc + 4 * k);
         }
 #pragma unroll
         for (int e = 0; e < EPL; ++e) ok[e] = true;
@@ -403,7 +423,7 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
 
     // new scales (:101-106)
     const float s_sm = (amax + 1e-12f) * d.inv_qm;            // == / 2^(bits-1), exact
-    const float s_sv = ((lmax - lmin) + 1e-12f) / d.qvf;      // IEEE division
+    const float s_sv = mdq_div_code_range((lmax - lmin) + 1e-12f, d.qvf, d.inv_qvf);  // == IEEE division
     const float s_vmin = lmin;
     if (j == 0 && blk_ok) {
         st_g<float>(s_sm, d.scale_m + blk);
@@ -471,7 +491,7 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
 #pragma unroll
         for (int e = 0; e < EPL; ++e) {
             const float qm = __builtin_amdgcn_fmed3f(qmf[e], -d.qm, d.qm - 1.0f);
-            const float qv = __builtin_amdgcn_fmed3f(qvf[e], 0.0f, d.qv);
+            const float qv = __builtin_amdgcn_fmed3f(qvf[e], 0.0f, d.qvf);
             if constexpr (ST == ST_P4) {
                 pk[e] = fma_(qv, 16.0f, qm + 8.0f);           // (v << 4) | (m + 8), exact
             } else {
@@ -506,13 +526,14 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
     }
 
     if constexpr (FULL && C::QPL > 0) {
+        const MdqDesc dt = tile_view<ST, GT>(d, tbase);
 #pragma unroll
         for (int k = 0; k < C::QPL; ++k) {
-            const int64_t i = base + 4 * (j + k * LPB);
-            if constexpr (ST == ST_P4) CodeIO<ST>::store4f(d, i, pk + 4 * k);
-            else CodeIO<ST>::store4(d, i, qmi + 4 * k, qvi + 4 * k);
+            const uint32_t i = lbase + 4 * (j + k * LPB);
+            if constexpr (ST == ST_P4) CodeIO<ST>::store4f(dt, i, pk + 4 * k);
+            else CodeIO<ST>::store4(dt, i, qmi + 4 * k, qvi + 4 * k);
             vf4 o = {pv[4 * k + 0], pv[4 * k + 1], pv[4 * k + 2], pv[4 * k + 3]};
-            st_nt<vf4>(o, d.p + i);
+            st_nt<vf4>(o, dt.p + i);
         }
     } else {
 #pragma unroll

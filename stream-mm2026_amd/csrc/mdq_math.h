@@ -79,8 +79,9 @@ MDQ_HD float mdq_logf(float x)
 {
     uint32_t ix = f_bits(x);
     int32_t t = (int32_t)(ix - 0x3f2aaaabu);
-    int32_t k = t >> 23;
-    float f = bits_f(((uint32_t)t & 0x007fffffu) + 0x3f2aaaabu);
+    int32_t k = t >> 23;                            // in [-256, 255]
+    float f = bits_f(ix - (uint32_t)(k * 8388608)); // == (t & 0x7fffff) + 0x3f2aaaab
+
     float r = f - 1.0f;
     float kf = (float)k;
     float p = bits_f(0xbe05ac99u);
@@ -112,6 +113,17 @@ MDQ_HD float mdq_round_half_away(float u, float d, float inv_lo, float hd)
     const float k0 = floor_(fma_(u, inv_lo, 0.5f));
     const float R = fma_(-k0, d, u);
     return R >= hd ? k0 + 1.0f : k0;
+}
+
+// x / D correctly rounded for D = (float)(2^bits - 1), bits 1..32, given
+// y = RN(1/D): q = x*y is within an ulp, the fma residual x - q*D is exact,
+// and one correction q + r*y rounds to RN(x/D).  Checked against IEEE
+// division for every positive float x and every bits value.
+MDQ_HD float mdq_div_code_range(float x, float D, float y)
+{
+    const float q = x * y;
+    const float r = fma_(-q, D, x);
+    return fma_(r, y, q);
 }
 
 // The reciprocal of d stepped down by 4 ulp, for mdq_round_half_away.

@@ -19,7 +19,8 @@ from ._capi import ROUND_NEAREST, ROUND_STOCHASTIC, StqTensor, check, dtype_code
 __all__ = [
     "ROUND_NEAREST", "ROUND_STOCHASTIC", "TensorState", "MultiTensorPlan", "fused_step",
     "multi_tensor_step",
-    "device_math", "device_math_digests", "host_math", "host_round_half_away", "host_philox",
+    "device_math", "device_math_digests", "host_math", "host_round_half_away", "host_div_code_range",
+    "host_philox",
     "lib", "rounding_code",
 ]
 
@@ -230,6 +231,14 @@ def host_round_half_away(u, d, inv_ulps: int = 0):
     d = np.ascontiguousarray(d, dtype=np.float32)
     out = np.empty_like(u)
     lib().stq_host_round_half_away(u.ctypes.data, d.ctypes.data, out.ctypes.data, u.size, int(inv_ulps))
+    return out
+
+
+def host_div_code_range(x, bits: int):
+    import numpy as np
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty_like(x)
+    lib().stq_host_div_code_range(x.ctypes.data, out.ctypes.data, x.size, int(bits))
     return out
 
 

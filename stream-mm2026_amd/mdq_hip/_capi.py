@@ -40,6 +40,7 @@ EXPORTED_SYMBOLS = (
     "stq_device_math_digests",
     "stq_host_math",
     "stq_host_round_half_away",
+    "stq_host_div_code_range",
     "stq_host_philox4x32_10",
 )
 
@@ -114,6 +115,8 @@ def lib() -> ctypes.CDLL:
     L.stq_host_math.restype = None
     L.stq_host_round_half_away.argtypes = [vp, vp, vp, i64, i32]
     L.stq_host_round_half_away.restype = None
+    L.stq_host_div_code_range.argtypes = [vp, vp, i64, i32]
+    L.stq_host_div_code_range.restype = None
     L.stq_host_philox4x32_10.argtypes = [vp, vp, vp]
     L.stq_host_philox4x32_10.restype = None
     _lib = L

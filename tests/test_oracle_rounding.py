@@ -81,3 +81,16 @@ def test_fp32_method_small_brute_force():
         ref = round_half_away_f64(u.astype(np.float64) / dd.astype(np.float64))
         for inv in (-1, 0, 1):
             assert np.array_equal(mdq_hip.host_round_half_away(u, dd, inv), ref)
+
+
+@pytest.mark.parametrize("bits", list(range(1, 33)))
+def test_new_v_scale_division_is_ieee(bits):
+    """s_sv = X / (2^bits - 1) (stquant_kernel.cu:102): the kernel's residual-corrected
+    product must equal IEEE division.  Strided over all positive floats here; the
+    same check over every positive float and every bits value passed when the
+    method was adopted."""
+    step = 997 if bits in (4, 8, 16, 32) else 99991
+    x = np.arange(1, 0x7F800000, step, dtype=np.int64).astype(np.uint32).view(np.float32)
+    D = np.float32(2.0 ** bits - 1.0)
+    got = mdq_hip.host_div_code_range(x, bits)
+    assert np.array_equal(got.view(np.uint32), (x / D).astype(np.float32).view(np.uint32))
