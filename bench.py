@@ -211,6 +211,15 @@ def main():
     ms_per_step = wall / args.steps * 1e3
     value = N / (ms_per_step * 1e-3)
 
+    # HBM bytes per launch measured by rocprofv3 (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0,
+    # the factors that map a plain 4 GiB copy's counters to 4 GiB), committed under profiles/
+    traffic, traffic_src = None, None
+    prof_json = os.path.join(ROOT, "profiles", f"mdq_step_{args.config}_{w['gdt']}_p4_b{w['B']}.json")
+    if os.path.exists(prof_json):
+        with open(prof_json) as f:
+            traffic = json.load(f)["traffic_bytes"]
+        traffic_src = os.path.relpath(prof_json, ROOT)
+
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle) ...")
@@ -248,7 +257,8 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": traffic,
+            "traffic_source": traffic_src,
             "kernel_ms": kernel_ms,
             "algorithmic_bytes": alg_bytes,
         },

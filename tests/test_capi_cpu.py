@@ -1,0 +1,94 @@
+"""The C-ABI library loads, exports every symbol include/stquant_hip.h declares,
+and rejects bad arguments with the reference's messages before touching a GPU
+(no device work is issued by any call in this file)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import mdq_hip
+from mdq_hip import _capi
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "stquant_hip.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|void|const char \*)\s*(stq_\w+)\s*\(", text, re.M)))
+
+
+def test_exports_every_declared_symbol():
+    L = mdq_hip.lib()
+    names = declared_symbols()
+    assert len(names) >= 10
+    for name in names:
+        assert hasattr(L, name), name
+    assert set(names) == set(_capi.EXPORTED_SYMBOLS)
+    assert L.stq_abi_version() == 1
+
+
+FAKE = 0x1000  # never dereferenced: every call below fails argument checks first
+
+
+def call_single(numel=256, grad_dtype=0, grad_numel=None, ea_dt=3, ea_n=None, easq_dt=3, easq_n=0,
+                scales=2, step=1, bits=4, block=128, prof_n=0, rounding=0):
+    L = mdq_hip.lib()
+    grad_numel = numel if grad_numel is None else grad_numel
+    ea_n = numel if ea_n is None else ea_n
+    return L.stq_fused_mdq_adamw(
+        FAKE, FAKE, grad_dtype, grad_numel, numel, FAKE, ea_dt, ea_n, FAKE, easq_dt, easq_n,
+        FAKE, scales, FAKE, scales, FAKE, scales, 0.9, 0.999, 1e-3, 0.01, 1e-8, step, bits, block,
+        FAKE if prof_n else None, prof_n, rounding, 0, 0, None)
+
+
+def err():
+    return mdq_hip.lib().stq_last_error().decode()
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(ea_dt=5, easq_dt=3, easq_n=256), "MDQ: state must be packed4 (uint8+empty), (int8,uint8), (int16,uint16) or (int32,uint32), got Short / Byte bits=4"),
+    (dict(ea_n=255), "packed4: exp_avg numel must match parameters"),
+    (dict(prof_n=3), "profile_cycles needs >= 5 elements"),
+    (dict(block=96), "block_size must be a power of two"),
+    (dict(block=0), "block_size must be >= 1"),
+    (dict(scales=1), "scale_m / scale_v / v_min need ceil(numel / 128) = 2 elements"),
+    (dict(step=0), "step must be >= 1"),
+    (dict(ea_dt=4, easq_dt=3, easq_n=256, bits=9), "bits=9 does not fit the 8-bit code storage"),
+    (dict(grad_numel=255), "grad numel (255) must match parameters (256)"),
+    (dict(grad_dtype=7), "grad must be Float, BFloat16 or Half, got Int"),
+    (dict(rounding=2), "rounding must be 0 (nearest) or 1 (stochastic)"),
+    (dict(ea_dt=4, easq_dt=3, easq_n=10), "exp_avg / exp_avg_sq must hold numel (256) codes"),
+])
+def test_argument_errors(kw, msg):
+    assert call_single(**kw) == _capi.STQ_ERR_INVALID
+    assert msg in err()
+
+
+def test_block_size_above_1024_is_clamped_like_the_reference():
+    # min(block_size, 1024) (stquant_kernel.cu:421): 4096 -> 1024, so 1 scale suffices for 256
+    assert call_single(block=4096, scales=0) == _capi.STQ_ERR_INVALID
+    assert "ceil(numel / 1024) = 1" in err()
+
+
+def test_empty_calls_are_no_ops():
+    L = mdq_hip.lib()
+    assert call_single(numel=0, scales=0) == _capi.STQ_OK
+    assert L.stq_multi_tensor_mdq_adamw(None, 0, 0, 3, 3, 128, 0, 0, None, 0, None) == _capi.STQ_OK
+
+
+def test_multi_tensor_rejects_mixed_storage():
+    L = mdq_hip.lib()
+    arr = (_capi.StqTensor * 2)()
+    for i, s in enumerate(arr):
+        s.p = s.grad = s.exp_avg = s.scale_m = s.scale_v = s.v_min = FAKE
+        s.exp_avg_sq = FAKE if i else None
+        s.numel = s.grad_numel = s.exp_avg_numel = 256
+        s.exp_avg_sq_numel = 256 if i else 0
+        s.scale_m_numel = s.scale_v_numel = s.v_min_numel = 2
+        s.beta1, s.beta2, s.lr, s.weight_decay, s.eps = 0.9, 0.999, 1e-3, 0.0, 1e-8
+        s.step, s.bits = 1, 4
+    # tensor 0 is packed4 (empty v codes), tensor 1 would be uint8+uint8: not a valid pair
+    rc = L.stq_multi_tensor_mdq_adamw(arr, 2, 0, 3, 3, 128, 0, 0, None, 0, None)
+    assert rc == _capi.STQ_ERR_INVALID and "MDQ: state must be packed4" in err()
