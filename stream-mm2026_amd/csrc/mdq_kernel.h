@@ -260,6 +260,22 @@ __device__ __forceinline__ int32_t group_reduce(int32_t x)
     return x;
 }
 
+// Every lane of an aligned group of min(LANES, 64) lanes receives the value
+// of the group's first lane: ds_swizzle in bit mode (and-mask clears the low
+// lane bits) within 32 lanes, readfirstlane for a whole wave.
+template <int LANES>
+__device__ __forceinline__ float block_bcast(float x)
+{
+    if constexpr (LANES <= 1) {
+        return x;
+    } else if constexpr (LANES <= 32) {
+        constexpr int and_mask = 0x1F & ~(LANES - 1);
+        return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, x), and_mask));
+    } else {
+        return __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, x)));
+    }
+}
+
 struct ProfAcc {
     unsigned long long c[5];
 };
@@ -312,13 +328,20 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
     const int64_t base = blk << LOG2B;
     const bool blk_ok = FULL || base < n;
 
-    // old block scales (stquant_kernel.cu:67-69)
+    // old block scales (stquant_kernel.cu:67-69): the block's first lane of
+    // each wave loads them and the block's other lanes take them by broadcast
+    // (one active lane per block keeps the small loads from occupying the
+    // whole wave's address path).
     float sm = 0.0f, sv = 0.0f, vmin = 0.0f;
-    if (blk_ok) {
+    const bool loader = (LPB <= 64 ? j == 0 : lane == 0) && blk_ok;
+    if (loader) {
         sm = ld_g<float>(d.scale_m + blk);
         sv = ld_g<float>(d.scale_v + blk);
         vmin = ld_g<float>(d.v_min + blk);
     }
+    sm = block_bcast<LPB>(sm);
+    sv = block_bcast<LPB>(sv);
+    vmin = block_bcast<LPB>(vmin);
 
     float pv[EPL], gv[EPL], mc[EPL];
     uint32_t vc[EPL];
