@@ -11,6 +11,7 @@ import ctypes
 from dataclasses import dataclass
 from typing import Optional, Sequence
 
+import numpy as np
 import torch
 
 from . import _capi
@@ -114,13 +115,27 @@ class TensorState:
     tensor_id: int = 0
 
 
-class MultiTensorPlan:
-    """A packed ``stq_tensor`` array for a fixed set of tensors.
+# numpy mirror of ``stq_tensor`` (144 bytes, no padding): a plan's descriptor list
+# lives in one structured array whose columns are refreshed vectorised per step.
+STQ_TENSOR_DTYPE = np.dtype([
+    ("p", np.uint64), ("grad", np.uint64), ("exp_avg", np.uint64), ("exp_avg_sq", np.uint64),
+    ("scale_m", np.uint64), ("scale_v", np.uint64), ("v_min", np.uint64),
+    ("numel", np.int64), ("grad_numel", np.int64), ("exp_avg_numel", np.int64),
+    ("exp_avg_sq_numel", np.int64), ("scale_m_numel", np.int64), ("scale_v_numel", np.int64),
+    ("v_min_numel", np.int64),
+    ("beta1", np.float32), ("beta2", np.float32), ("lr", np.float32), ("weight_decay", np.float32),
+    ("eps", np.float32), ("step", np.int32), ("bits", np.int32), ("tensor_id", np.uint32),
+])
+assert STQ_TENSOR_DTYPE.itemsize == ctypes.sizeof(StqTensor)
 
-    Building the array costs a few microseconds per tensor; a plan is built
-    once and re-run, with only the per-tensor step (and optionally the grad
-    pointers) refreshed per call.  The tensors must stay alive and keep their
-    storage while the plan is used.
+
+class MultiTensorPlan:
+    """The ``stq_tensor`` list of a fixed set of tensors, ready to launch.
+
+    Validation and pointer extraction happen once; per call only the columns
+    that change between steps are refreshed (``set_steps``, ``set_grads``,
+    ``set_hparams``).  The tensors must stay alive and keep their storage while
+    the plan is used.
     """
 
     def __init__(self, entries: Sequence[TensorState], block_size: int, *,
@@ -134,12 +149,25 @@ class MultiTensorPlan:
         self.device = self.entries[0].p.device if self.entries else None
 
     def set_steps(self, steps) -> None:
-        if isinstance(steps, int):
-            for i in range(self.n):
-                self.arr[i].step = steps
-        else:
-            for i, s in enumerate(steps):
-                self.arr[i].step = int(s)
+        self.arr["step"] = steps
+
+    def set_grads(self, grads: Sequence[torch.Tensor]) -> None:
+        """New grad tensors of the same dtype and size (autograd reallocates them)."""
+        gdt = self.codes[0]
+        if len(grads) != self.n:
+            raise RuntimeError("set_grads: one grad per planned tensor")
+        numel = self.arr["numel"]
+        for i, g in enumerate(grads):
+            if dtype_code(g.dtype) != gdt or g.numel() != numel[i] or not g.is_contiguous() \
+                    or g.device != self.device:
+                raise RuntimeError("set_grads: grad must match the planned dtype, size and device")
+        self.arr["grad"] = [g.data_ptr() for g in grads]
+
+    def set_hparams(self, lr=None, beta1=None, beta2=None, eps=None, weight_decay=None, bits=None) -> None:
+        for name, v in (("lr", lr), ("beta1", beta1), ("beta2", beta2), ("eps", eps),
+                        ("weight_decay", weight_decay), ("bits", bits)):
+            if v is not None:
+                self.arr[name] = v
 
     def run(self, profile_cycles: Optional[torch.Tensor] = None) -> None:
         if self.n == 0:
@@ -148,21 +176,21 @@ class MultiTensorPlan:
         gdt, eadt, easqdt = self.codes
         with torch.cuda.device(self.device):
             rc = lib().stq_multi_tensor_mdq_adamw(
-                self.arr, self.n, gdt, eadt, easqdt, self.block_size, self.rounding, self.seed,
-                prof_ptr, prof_n, _capi.stream_handle(self.device))
+                self.arr.ctypes.data_as(ctypes.POINTER(StqTensor)), self.n, gdt, eadt, easqdt,
+                self.block_size, self.rounding, self.seed, prof_ptr, prof_n, _capi.stream_handle(self.device))
         check(rc)
 
 
 def _pack_entries(entries: Sequence[TensorState]):
     n = len(entries)
-    arr = (StqTensor * max(n, 1))()
+    arr = np.zeros(n, dtype=STQ_TENSOR_DTYPE)
     if n == 0:
         return arr, (0, 0, 0)
     e0 = entries[0]
     dev = e0.p.device
     gdt, eadt, easqdt = e0.grad.dtype, e0.exp_avg.dtype, e0.exp_avg_sq.dtype
-    arr = (StqTensor * n)()
-    for i, e in enumerate(entries):
+    rows = []
+    for e in entries:
         if e.p.device != dev or e.grad.device != dev:
             raise RuntimeError("multi_tensor_step: all tensors must be on one device")
         if e.grad.dtype != gdt or e.exp_avg.dtype != eadt or e.exp_avg_sq.dtype != easqdt:
@@ -174,17 +202,15 @@ def _pack_entries(entries: Sequence[TensorState]):
                         ("scale_v", e.scale_v), ("v_min", e.v_min)):
             if not t.is_contiguous():
                 raise RuntimeError(f"{name} must be contiguous")
-        s = arr[i]
-        s.p = e.p.data_ptr(); s.grad = e.grad.data_ptr()
-        s.exp_avg = e.exp_avg.data_ptr()
-        s.exp_avg_sq = e.exp_avg_sq.data_ptr() if e.exp_avg_sq.numel() else None
-        s.scale_m = e.scale_m.data_ptr(); s.scale_v = e.scale_v.data_ptr(); s.v_min = e.v_min.data_ptr()
-        s.numel = e.p.numel(); s.grad_numel = e.grad.numel()
-        s.exp_avg_numel = e.exp_avg.numel(); s.exp_avg_sq_numel = e.exp_avg_sq.numel()
-        s.scale_m_numel = e.scale_m.numel(); s.scale_v_numel = e.scale_v.numel()
-        s.v_min_numel = e.v_min.numel()
-        s.beta1 = e.beta1; s.beta2 = e.beta2; s.lr = e.lr; s.weight_decay = e.weight_decay; s.eps = e.eps
-        s.step = int(e.step); s.bits = int(e.bits); s.tensor_id = int(e.tensor_id) & 0xFFFFFFFF
+        rows.append((
+            e.p.data_ptr(), e.grad.data_ptr(), e.exp_avg.data_ptr(),
+            e.exp_avg_sq.data_ptr() if e.exp_avg_sq.numel() else 0,
+            e.scale_m.data_ptr(), e.scale_v.data_ptr(), e.v_min.data_ptr(),
+            e.p.numel(), e.grad.numel(), e.exp_avg.numel(), e.exp_avg_sq.numel(),
+            e.scale_m.numel(), e.scale_v.numel(), e.v_min.numel(),
+            e.beta1, e.beta2, e.lr, e.weight_decay, e.eps, int(e.step), int(e.bits),
+            int(e.tensor_id) & 0xFFFFFFFF))
+    arr[:] = rows
     return arr, (dtype_code(gdt), dtype_code(eadt), dtype_code(easqdt))
 
 

@@ -16,8 +16,9 @@ those of the reference kernel (:246-263 -> stquant_kernel.cu).
 New optional param-group keys (defaults keep the reference behaviour):
 ``bits`` (fixed code width 4/8/16/32 instead of the score-based choice),
 ``rounding`` ('nearest' or 'stochastic') and ``seed`` (stochastic stream).
-``sync_timing=False`` skips the two device synchronisations that fill the
-timing dict.
+``sync_timing=False`` skips the device synchronisations that fill the timing
+dict (and the kernel phase profile), so ``step()`` issues its work
+asynchronously on the current stream.
 """
 from __future__ import annotations
 
@@ -295,7 +296,14 @@ class MDQAdamWSimple(Optimizer):
 
     def _run_kernels(self, items):
         """Group tensors by (device, code storage, grad dtype, block size,
-        rounding, seed) and run one multi-tensor launch per group."""
+        rounding, seed) and run one multi-tensor launch per group.
+
+        Each group's launch plan is cached and reused while its tensors and
+        their state tensors stay the same objects (bit-width transitions replace
+        state tensors and so rebuild the plan); per step only the grad
+        pointers, steps, bit widths and hyper-parameters are refreshed.  Plans
+        keep no reference to gradients.
+        """
         buckets = OrderedDict()
         for p, group in items:
             state = self.state[p]
@@ -304,22 +312,48 @@ class MDQAdamWSimple(Optimizer):
                 raise RuntimeError("MDQAdamWSimple does not support sparse gradients")
             if not grad.is_contiguous():
                 grad = grad.contiguous()
-            bsz = min(int(group["block_size"]), 1024)
-            rnd = mdq_hip.rounding_code(group.get("rounding", "nearest"))
-            seed = int(group.get("seed", 0) or 0)
             ea, easq = state["exp_avg"], state["exp_avg_sq"]
-            key = (p.device, ea.dtype, easq.dtype, easq.numel() == 0, grad.dtype, bsz, rnd, seed)
-            b1, b2 = group["betas"]
-            buckets.setdefault(key, []).append(mdq_hip.TensorState(
-                p=p, grad=grad, exp_avg=ea, exp_avg_sq=easq, scale_m=state["scale_m"],
-                scale_v=state["scale_v"], v_min=state["v_min"], step=state["step"],
-                bits=int(state["current_bit"]), lr=group["lr"], beta1=b1, beta2=b2, eps=group["eps"],
-                weight_decay=group["weight_decay"], tensor_id=self._tensor_ids.get(p, 0)))
-        for (dev, _ea, _easq, _packed, _gdt, bsz, rnd, seed), entries in buckets.items():
+            key = (p.device, ea.dtype, easq.dtype, easq.numel() == 0, grad.dtype,
+                   min(int(group["block_size"]), 1024), mdq_hip.rounding_code(group.get("rounding", "nearest")),
+                   int(group.get("seed", 0) or 0))
+            buckets.setdefault(key, []).append((p, group, state, grad))
+        cache = self.__dict__.setdefault("_plan_cache", {})
+        ids = self._tensor_ids
+        for key, lst in buckets.items():
+            dev, bsz, rnd, seed = key[0], key[5], key[6], key[7]
+            sig = tuple((id(p), id(st["exp_avg"]), id(st["exp_avg_sq"]), id(st["scale_m"]),
+                         id(st["scale_v"]), id(st["v_min"])) for p, _g, st, _gr in lst)
+            plan = cache.get(key)
+            if plan is None or plan.sig != sig:
+                entries = [mdq_hip.TensorState(
+                    p=p, grad=gr, exp_avg=st["exp_avg"], exp_avg_sq=st["exp_avg_sq"], scale_m=st["scale_m"],
+                    scale_v=st["scale_v"], v_min=st["v_min"], step=st["step"], bits=int(st["current_bit"]),
+                    lr=g["lr"], beta1=g["betas"][0], beta2=g["betas"][1], eps=g["eps"],
+                    weight_decay=g["weight_decay"], tensor_id=ids.get(p, 0)) for p, g, st, gr in lst]
+                plan = mdq_hip.MultiTensorPlan(entries, bsz, rounding=rnd, seed=seed)
+                plan.entries = None          # no references to grads
+                # Strong references to the params and state tensors the plan points
+                # at: while they are held no other object can reuse their id(), so
+                # the id signature identifies exactly these tensors.
+                plan.keep = [(p, st["exp_avg"], st["exp_avg_sq"], st["scale_m"], st["scale_v"], st["v_min"])
+                             for p, _g, st, _gr in lst]
+                plan.sig = sig
+                cache[key] = plan
+            else:
+                plan.set_grads([gr for _p, _g, _st, gr in lst])
+                plan.set_steps([st["step"] for _p, _g, st, _gr in lst])
+                plan.set_hparams(
+                    lr=[g["lr"] for _p, g, _st, _gr in lst], beta1=[g["betas"][0] for _p, g, _st, _gr in lst],
+                    beta2=[g["betas"][1] for _p, g, _st, _gr in lst], eps=[g["eps"] for _p, g, _st, _gr in lst],
+                    weight_decay=[g["weight_decay"] for _p, g, _st, _gr in lst],
+                    bits=[int(st["current_bit"]) for _p, _g, st, _gr in lst])
             prof = None
-            if self._kernel_profile_buf is not None and self._kernel_profile_device == dev:
+            if self.sync_timing and self._kernel_profile_buf is not None and self._kernel_profile_device == dev:
                 prof = self._kernel_profile_buf
-            mdq_hip.multi_tensor_step(entries, bsz, rounding=rnd, seed=seed, profile_cycles=prof)
+            plan.run(prof)
+        # plans of buckets that no longer exist keep pointers to dropped tensors
+        for key in [k for k in cache if k not in buckets]:
+            del cache[key]
 
     @property
     def _tensor_ids(self):
@@ -565,8 +599,10 @@ class MDQAdamWSimple(Optimizer):
         lt["mdq_bit_decision_ms"] = allreduce_ms + score_bits_ms
         lt["mdq_extra_stats_ms"] = grad_stats_ms + allreduce_ms + score_bits_ms
 
+        # Phase profiling needs the cycle buffer read back (a device sync), so it
+        # is on only with sync_timing, as the reference always has it.
         profile_device = None
-        if params_with_grad:
+        if params_with_grad and self.sync_timing:
             profile_device = params_with_grad[0][0].device
             if profile_device.type == "cuda":
                 self._reset_kernel_profile(profile_device)
