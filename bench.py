@@ -72,6 +72,36 @@ CONFIGS = {
 }
 
 
+def config5_sizes():
+    """257 sizes, log-uniform in [1, 2^24] (seed 0): 363,174,740 params,
+    254 of them not a multiple of 128."""
+    import numpy as np
+    rng = np.random.default_rng(0)
+    return np.clip(np.floor(np.exp(rng.uniform(0, np.log(2 ** 24), 257))), 1, 2 ** 24).astype(np.int64).tolist()
+
+
+def config5_grads_numpy(n: int, B: int, rng):
+    """1e-3 * Student-t(df=3); 5 % of the quant blocks all zero; 0.1 % of elements x 1000."""
+    import numpy as np
+    g = (rng.standard_t(3, n) * 1e-3).astype(np.float32)
+    nb = (n + B - 1) // B
+    g[np.repeat(rng.random(nb) < 0.05, B)[:n]] = 0.0
+    g[rng.random(n) < 0.001] *= 1000.0
+    return g
+
+
+def config5_grads_device(n: int, B: int, gen, dev):
+    """The config-5 grad recipe drawn on the device (t = z / sqrt(chi2_3 / 3))."""
+    import torch
+    z = torch.randn(4, n, device=dev, generator=gen)
+    g = z[0] / torch.sqrt((z[1] ** 2 + z[2] ** 2 + z[3] ** 2) / 3.0) * 1e-3
+    nb = (n + B - 1) // B
+    zero = torch.rand(nb, device=dev, generator=gen) < 0.05
+    g[zero.repeat_interleave(B)[:n]] = 0.0
+    g[torch.rand(n, device=dev, generator=gen) < 0.001] *= 1000.0
+    return g.contiguous()
+
+
 def bytes_per_param(grad_bytes: int, bits: int, block: int) -> float:
     """Algorithmic HBM bytes per param per step: p read+write (8), grad read,
     codes read+write (1+1 packed 4-bit, 2+2 at 8 bits), and the three fp32
@@ -119,6 +149,77 @@ def build_workload(name, dev, seed=0):
                 grad_bytes=2 if gdt == "bf16" else 4, keep=(p, g, codes, sm, sv, vm))
 
 
+ALIGN_ELEMS = 256
+
+
+def sweep_config5(dev, steps: int, warmup: int):
+    """Config 5 over {4, 8}-bit x B {64, 128, 256} x {nearest, stochastic}: ms/step, GB/s, params/s."""
+    import torch
+
+    import mdq_hip
+
+    sizes = config5_sizes()
+    N = sum(sizes)
+    gen = torch.Generator(device=dev).manual_seed(5)
+    points = []
+    for B in (64, 128, 256):
+        # each tensor starts on a 1 KiB boundary of p, as separate torch allocations would
+        offs = [0]
+        for n in sizes:
+            offs.append(offs[-1] + (n + ALIGN_ELEMS - 1) // ALIGN_ELEMS * ALIGN_ELEMS)
+        NP = offs[-1]
+        p = torch.empty(NP, dtype=torch.float32, device=dev).normal_(0.0, 0.02, generator=gen)
+        g = torch.zeros(NP, dtype=torch.float32, device=dev)
+        for n, o in zip(sizes, offs):
+            g[o:o + n] = config5_grads_device(n, B, gen, dev)
+        nbs = [(n + B - 1) // B for n in sizes]
+        NB = sum(nbs)
+        for bits in (4, 8):
+            if bits == 4:
+                cm = torch.full((NP,), 0x08, dtype=torch.uint8, device=dev)
+                cv = torch.empty(0, dtype=torch.uint8, device=dev)
+            else:
+                cm = torch.zeros(NP, dtype=torch.int8, device=dev)
+                cv = torch.zeros(NP, dtype=torch.uint8, device=dev)
+            sm = torch.zeros(NB, device=dev)
+            sv = torch.zeros(NB, device=dev)
+            vm = torch.full((NB,), -20.0, device=dev)
+            entries, ob = [], 0
+            for i, (n, nb, o) in enumerate(zip(sizes, nbs, offs)):
+                entries.append(mdq_hip.TensorState(
+                    p[o:o + n], g[o:o + n], cm[o:o + n], cv if bits == 4 else cv[o:o + n],
+                    sm[ob:ob + nb], sv[ob:ob + nb], vm[ob:ob + nb], 1, bits, 1e-3, 0.9, 0.999, 1e-8, 0.01, i))
+                ob += nb
+            for rounding in ("nearest", "stochastic"):
+                plan = mdq_hip.MultiTensorPlan(entries, B, rounding=rounding, seed=7)
+                step = 0
+                for _ in range(warmup):
+                    step += 1
+                    plan.set_steps(step)
+                    plan.run()
+                torch.cuda.synchronize()
+                ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                ev0.record()
+                for _ in range(steps):
+                    step += 1
+                    plan.set_steps(step)
+                    plan.run()
+                ev1.record()
+                torch.cuda.synchronize()
+                ms = ev0.elapsed_time(ev1) / steps
+                bpp = bytes_per_param(4, bits, B)
+                pt = dict(bits=bits, block=B, rounding=rounding, ms=ms, params_per_s=N / (ms * 1e-3),
+                          bytes_per_param=bpp, gbs=bpp * N / (ms * 1e-3) / 1e9,
+                          pct_peak=100 * bpp * N / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS)
+                log(f"config5 bits={bits} B={B} {rounding}: {ms:.3f} ms, {pt['gbs']:.0f} GB/s "
+                    f"({pt['pct_peak']:.1f} %), {pt['params_per_s']:.3e} params/s")
+                points.append(pt)
+            del cm, cv, sm, sv, vm, entries, plan
+        del p, g
+        torch.cuda.empty_cache()
+    return dict(params=N, tensors=len(sizes), points=points)
+
+
 def cpu_baseline(gdt: str, bits: int, B: int, seconds: float):
     """The oracle (C, OpenMP over quant blocks) on a 2^24-param slice of the same
     workload, repeated for about `seconds`; params/s over this host's cores."""
@@ -154,6 +255,8 @@ def main():
     ap.add_argument("--config", default="llama7b", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--sweep-config5", action="store_true",
+                    help="time BASELINE config 5 over bits x block x rounding (one JSON line with all points)")
     ap.add_argument("--copy-gib", type=float, default=0.0,
                     help="also run a plain device-to-device copy of this many GiB (rocprof calibration)")
     args = ap.parse_args()
@@ -166,6 +269,11 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.sweep_config5:
+        res = sweep_config5(dev, args.steps, args.warmup)
+        print(json.dumps({"metric": "config 5 sweep: params/s and HBM GB/s per point", "n_gpus": 1,
+                          "steps": args.steps, "warmup": args.warmup, "data": "synthetic", **res}), flush=True)
+        return
     w = build_workload(args.config, dev)
     plan = w["plan"]
     torch.cuda.synchronize()
