@@ -220,6 +220,41 @@ def sweep_config5(dev, steps: int, warmup: int):
     return dict(params=N, tensors=len(sizes), points=points)
 
 
+def e2e_gpt2(steps: int, warmup: int, out_path):
+    """GPT-2 small, seq 1024, micro-batch 8, bf16 autocast, 4-bit fused AdamW
+    with stochastic rounding vs the same optimizer in nearest mode (the reference's arithmetic) and
+    torch AdamW, each on identical seeded synthetic tokens."""
+    import gpt2_pretrain
+
+    runs = {}
+    for key, name, rounding in (("mdq4_stochastic", "MDQAdamW-Simple-FusedIO", "stochastic"),
+                                ("mdq4_nearest", "MDQAdamW-Simple-FusedIO", "nearest"),
+                                ("adamw32", "AdamW-32bit", None)):
+        log(f"gpt2 e2e: {key} ({steps} steps)")
+        runs[key] = gpt2_pretrain.train(name, steps=steps, warmup=warmup, rounding=rounding or "nearest",
+                                        log_every=50)
+    la = runs["mdq4_stochastic"]["History"]["loss"]
+    lb = runs["mdq4_nearest"]["History"]["loss"]
+    lc = runs["adamw32"]["History"]["loss"]
+    res = {
+        "metric": "GPT-2 small e2e: optimizer share of step time and loss-curve gap", "n_gpus": 1,
+        "steps": steps, "warmup": warmup, "dtype": "bf16 autocast, fp32 optimizer math",
+        "data": "synthetic uniform tokens (seeded, identical across runs)",
+        "config": {"workload": "gpt2-small e2e", "global_batch": 8, "seq_len": 1024, "bits": 4, "block": 128},
+        "loss_gap_stochastic_vs_nearest": {
+            "max_rel_smoothed10": gpt2_pretrain.compare_loss_curves(la, lb, 10),
+            "max_rel_per_step": gpt2_pretrain.compare_loss_curves(la, lb, 1)},
+        "loss_gap_stochastic_vs_adamw32": {
+            "max_rel_smoothed10": gpt2_pretrain.compare_loss_curves(la, lc, 10),
+            "max_rel_per_step": gpt2_pretrain.compare_loss_curves(la, lc, 1)},
+        "runs": {k: {kk: vv for kk, vv in v.items() if kk != "History"} for k, v in runs.items()},
+    }
+    if out_path:
+        with open(out_path, "w") as f:
+            json.dump({**res, "loss": {k: v["History"]["loss"] for k, v in runs.items()}}, f, indent=1)
+    return res
+
+
 def cpu_baseline(gdt: str, bits: int, B: int, seconds: float):
     """The oracle (C, OpenMP over quant blocks) on a 2^24-param slice of the same
     workload, repeated for about `seconds`; params/s over this host's cores."""
@@ -257,6 +292,10 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--sweep-config5", action="store_true",
                     help="time BASELINE config 5 over bits x block x rounding (one JSON line with all points)")
+    ap.add_argument("--e2e-gpt2", action="store_true",
+                    help="BASELINE config 3: GPT-2 small pretraining, stochastic vs nearest vs AdamW")
+    ap.add_argument("--e2e-steps", type=int, default=300)
+    ap.add_argument("--e2e-out", default=None, help="also write the loss histories as JSON here")
     ap.add_argument("--copy-gib", type=float, default=0.0,
                     help="also run a plain device-to-device copy of this many GiB (rocprof calibration)")
     args = ap.parse_args()
@@ -273,6 +312,9 @@ def main():
         res = sweep_config5(dev, args.steps, args.warmup)
         print(json.dumps({"metric": "config 5 sweep: params/s and HBM GB/s per point", "n_gpus": 1,
                           "steps": args.steps, "warmup": args.warmup, "data": "synthetic", **res}), flush=True)
+        return
+    if args.e2e_gpt2:
+        print(json.dumps(e2e_gpt2(args.e2e_steps, args.warmup, args.e2e_out)), flush=True)
         return
     w = build_workload(args.config, dev)
     plan = w["plan"]

@@ -147,6 +147,9 @@ class MultiTensorPlan:
         self.entries = list(entries)
         self.arr, self.codes = _pack_entries(self.entries)
         self.device = self.entries[0].p.device if self.entries else None
+        self._grad_dtype = self.entries[0].grad.dtype if self.entries else None
+        self._dev_index = self.entries[0].p.get_device() if self.entries else -1
+        self._numel = self.arr["numel"].tolist()
 
     def set_steps(self, steps) -> None:
         self.arr["step"] = steps
@@ -162,6 +165,20 @@ class MultiTensorPlan:
                     or g.device != self.device:
                 raise RuntimeError("set_grads: grad must match the planned dtype, size and device")
         self.arr["grad"] = [g.data_ptr() for g in grads]
+
+    def try_set_grads(self, grads: Sequence[torch.Tensor]) -> bool:
+        """``set_grads`` that returns False (and changes nothing) instead of raising."""
+        if len(grads) != self.n:
+            return False
+        tdt, di = self._grad_dtype, self._dev_index
+        ptrs = []
+        for g, n in zip(grads, self._numel):
+            if g is None or g.dtype is not tdt or g.get_device() != di or g.numel() != n \
+                    or not g.is_contiguous():
+                return False
+            ptrs.append(g.data_ptr())
+        self.arr["grad"] = ptrs
+        return True
 
     def set_hparams(self, lr=None, beta1=None, beta2=None, eps=None, weight_decay=None, bits=None) -> None:
         for name, v in (("lr", lr), ("beta1", beta1), ("beta2", beta2), ("eps", eps),

@@ -9,34 +9,11 @@ and the fast-path ratio are reported in the timing dict.
 """
 from __future__ import annotations
 
-import torch
-
 from stquant_opt_simple import MDQAdamWSimple
 
 
 class MDQAdamWSimpleFusedIO(MDQAdamWSimple):
     """MDQ Simple + the no-pack/unpack fast path when the storage already fits."""
-
-    @classmethod
-    def _storage_matches_bits(cls, state, bits: int) -> bool:
-        # stquant_opt_fused_io.py:19-37
-        if "exp_avg" not in state:
-            return False
-        ea, easq = state["exp_avg"], state.get("exp_avg_sq")
-        if bits == 4:
-            return cls._is_momentum_packed4(state)
-        if bits == 8:
-            return (
-                ea.dtype == torch.int8
-                and easq is not None
-                and easq.dtype == torch.uint8
-                and easq.numel() == ea.numel()
-            )
-        if bits == 16:
-            return ea.dtype == torch.int16 and easq is not None and easq.dtype == torch.uint16
-        if bits >= 32:
-            return ea.dtype == torch.int32 and easq is not None and easq.dtype == torch.uint32
-        return False
 
     def _prepare_update(self, p, group):
         # stquant_opt_fused_io.py:39-54
@@ -49,6 +26,10 @@ class MDQAdamWSimpleFusedIO(MDQAdamWSimple):
             return super()._prepare_update(p, group)
         lt["mdq_fused_io_fast_path_params"] = lt.get("mdq_fused_io_fast_path_params", 0) + 1
         return False
+
+    def _count_steady_params(self, n: int) -> None:
+        # a steady step only runs tensors whose storage already matches
+        self.last_step_timings["mdq_fused_io_fast_path_params"] = n
 
     def _finalize_step_timings(self, profile_device):
         # stquant_opt_fused_io.py:86-93

@@ -26,6 +26,7 @@ import math
 import time
 from collections import OrderedDict
 
+import numpy as np
 import torch
 import torch.distributed as dist
 from torch.optim import Optimizer
@@ -81,6 +82,12 @@ class MDQAdamWSimple(Optimizer):
         self._kernel_profile_device = None
 
     _KERNEL_PROF_SLOTS = 5
+    # launch-plan class of ``_run_kernels`` (a test harness substitutes its own executor)
+    _plan_cls = mdq_hip.MultiTensorPlan
+
+    def add_param_group(self, param_group):
+        self.__dict__["_steady"] = None
+        super().add_param_group(param_group)
 
     # ------------------------------------------------------------------
     # kernel phase profile (stquant_opt_simple.py:56-83)
@@ -142,6 +149,28 @@ class MDQAdamWSimple(Optimizer):
             return False
         ea, easq = state["exp_avg"], state["exp_avg_sq"]
         return ea.dtype == torch.uint8 and easq.numel() == 0 and ea.numel() > 0
+
+    @classmethod
+    def _storage_matches_bits(cls, state, bits: int) -> bool:
+        """True when the code storage is already the one ``bits`` uses
+        (stquant_opt_fused_io.py:19-37); aligning and re-packing are no-ops then."""
+        if "exp_avg" not in state:
+            return False
+        ea, easq = state["exp_avg"], state.get("exp_avg_sq")
+        if bits == 4:
+            return cls._is_momentum_packed4(state)
+        if bits == 8:
+            return (
+                ea.dtype == torch.int8
+                and easq is not None
+                and easq.dtype == torch.uint8
+                and easq.numel() == ea.numel()
+            )
+        if bits == 16:
+            return ea.dtype == torch.int16 and easq is not None and easq.dtype == torch.uint16
+        if bits >= 32:
+            return ea.dtype == torch.int32 and easq is not None and easq.dtype == torch.uint32
+        return False
 
     @staticmethod
     def _unpack_packed4_momentum(state):
@@ -259,14 +288,15 @@ class MDQAdamWSimple(Optimizer):
         alignment of stquant_opt_simple.py:231-239.  Returns True when the
         storage must be re-packed after the kernel (:269).
 
-        A packed-nibble state at bits == 4 is handed to the packed kernel
-        directly: unpack -> int8/uint8 kernel -> re-pack (the reference's route)
-        yields the same codes, scales and params byte for byte.
+        A state whose storage already fits ``bits`` is handed to the kernel
+        as it is: for packed nibbles at 4 bits, unpack -> int8/uint8 kernel ->
+        re-pack (the reference's route) yields the same codes, scales and params
+        byte for byte; for the other widths aligning and packing change nothing.
         """
         state = self.state[p]
         bits = int(state["current_bit"])
         state["step"] += 1
-        if bits == 4 and self._is_momentum_packed4(state):
+        if self._storage_matches_bits(state, bits):
             return False
         self._align_momentum_storage(state, bits)
         return True
@@ -296,7 +326,8 @@ class MDQAdamWSimple(Optimizer):
 
     def _run_kernels(self, items):
         """Group tensors by (device, code storage, grad dtype, block size,
-        rounding, seed) and run one multi-tensor launch per group.
+        rounding, seed) and run one multi-tensor launch per group; returns
+        ``[(plan, indices into items), ...]``.
 
         Each group's launch plan is cached and reused while its tensors and
         their state tensors stay the same objects (bit-width transitions replace
@@ -305,7 +336,7 @@ class MDQAdamWSimple(Optimizer):
         keep no reference to gradients.
         """
         buckets = OrderedDict()
-        for p, group in items:
+        for i, (p, group) in enumerate(items):
             state = self.state[p]
             grad = p.grad
             if grad.is_sparse:
@@ -316,10 +347,13 @@ class MDQAdamWSimple(Optimizer):
             key = (p.device, ea.dtype, easq.dtype, easq.numel() == 0, grad.dtype,
                    min(int(group["block_size"]), 1024), mdq_hip.rounding_code(group.get("rounding", "nearest")),
                    int(group.get("seed", 0) or 0))
-            buckets.setdefault(key, []).append((p, group, state, grad))
+            buckets.setdefault(key, []).append((p, group, state, grad, i))
         cache = self.__dict__.setdefault("_plan_cache", {})
         ids = self._tensor_ids
+        runs = []
         for key, lst in buckets.items():
+            lst = [x[:4] for x in lst]
+            idx = [x[4] for x in buckets[key]]
             dev, bsz, rnd, seed = key[0], key[5], key[6], key[7]
             sig = tuple((id(p), id(st["exp_avg"]), id(st["exp_avg_sq"]), id(st["scale_m"]),
                          id(st["scale_v"]), id(st["v_min"])) for p, _g, st, _gr in lst)
@@ -330,7 +364,7 @@ class MDQAdamWSimple(Optimizer):
                     scale_v=st["scale_v"], v_min=st["v_min"], step=st["step"], bits=int(st["current_bit"]),
                     lr=g["lr"], beta1=g["betas"][0], beta2=g["betas"][1], eps=g["eps"],
                     weight_decay=g["weight_decay"], tensor_id=ids.get(p, 0)) for p, g, st, gr in lst]
-                plan = mdq_hip.MultiTensorPlan(entries, bsz, rounding=rnd, seed=seed)
+                plan = self._plan_cls(entries, bsz, rounding=rnd, seed=seed)
                 plan.entries = None          # no references to grads
                 # Strong references to the params and state tensors the plan points
                 # at: while they are held no other object can reuse their id(), so
@@ -351,9 +385,11 @@ class MDQAdamWSimple(Optimizer):
             if self.sync_timing and self._kernel_profile_buf is not None and self._kernel_profile_device == dev:
                 prof = self._kernel_profile_buf
             plan.run(prof)
+            runs.append((plan, idx))
         # plans of buckets that no longer exist keep pointers to dropped tensors
         for key in [k for k in cache if k not in buckets]:
             del cache[key]
+        return runs
 
     @property
     def _tensor_ids(self):
@@ -463,6 +499,8 @@ class MDQAdamWSimple(Optimizer):
         state tensor to the param dtype, turning integer codes into float32.
         The code values are small integers (exact in float32); each code tensor
         is cast back to the integer dtype it had in ``state_dict``."""
+        self._steady = None
+        self.__dict__.pop("_plan_cache", None)
         saved_dtypes = {}
         for pid, st in state_dict.get("state", {}).items():
             saved_dtypes[pid] = {k: st[k].dtype for k in self._CODE_KEYS
@@ -515,6 +553,20 @@ class MDQAdamWSimple(Optimizer):
         update_decision = (self.total_steps % update_freq == 0) or (self.total_steps < 5)
         self.last_step_timings["mdq_update_decision"] = update_decision
         self.last_step_timings["mdq_update_freq"] = update_freq
+
+        sc = self._steady_lookup(update_decision)
+        if sc is not None:
+            for key in ("mdq_grad_stats_ms", "mdq_allreduce_ms", "mdq_score_bits_ms", "mdq_stats_ms",
+                        "mdq_bit_decision_ms", "mdq_extra_stats_ms"):
+                self.last_step_timings[key] = 0.0
+            dev = sc["params"][0].device
+            profile_device = dev if self.sync_timing and dev.type == "cuda" else None
+            if profile_device is not None:
+                self._reset_kernel_profile(profile_device)
+            if self._steady_step(sc):
+                self._finalize_step_timings(profile_device)
+                return loss
+        self._steady = None
 
         params_with_grad = []
         all_stats = []
@@ -625,7 +677,7 @@ class MDQAdamWSimple(Optimizer):
         if self.sync_timing:
             self._sync_device(dev)
         tk0 = time.perf_counter()
-        self._run_kernels(params_with_grad)
+        runs = self._run_kernels(params_with_grad)
         if self.sync_timing:
             self._sync_device(dev)
         kernel_ms = (time.perf_counter() - tk0) * 1000.0
@@ -638,3 +690,96 @@ class MDQAdamWSimple(Optimizer):
         lt["quant_dequant_unpack_ms"] += unpack_ms
         lt["quant_dequant_kernel_ms"] += kernel_ms
         lt["quant_dequant_pack_ms"] += pack_ms
+        # No storage was replaced: the plans just launched describe the state as
+        # it stands, so the next step can reuse them (``_steady_step``).
+        self._steady = self._make_steady(params_with_grad, runs) if runs and not any(repack) else None
+
+    # ------------------------------------------------------------------
+    # steady state: same tensors, same storage, same bit widths as last step
+    # ------------------------------------------------------------------
+    def _group_cfg(self):
+        return tuple((g.get("bits"), min(int(g.get("block_size", 256)), 1024), g.get("rounding", "nearest"),
+                      g.get("seed", 0)) for g in self.param_groups)
+
+    def _make_steady(self, params_with_grad, runs):
+        gpos = {id(g): k for k, g in enumerate(self.param_groups)}
+        states = [self.state[p] for p, _g in params_with_grad]
+        return {
+            "ids": [id(p) for p, _g in params_with_grad],
+            "params": [p for p, _g in params_with_grad],
+            "states": states,
+            "state_obj": self.state,
+            "cfg": self._group_cfg(),
+            "runs": [(plan, idx, np.array([gpos[id(params_with_grad[i][1])] for i in idx], np.int64))
+                     for plan, idx in runs],
+        }
+
+    def _steady_lookup(self, update_decision: bool):
+        """The cached steady state if this step may reuse it, else None.
+
+        Reuse needs: the same param objects with grads in the same order, the
+        same ``state`` dict, the same per-group bits / block size / rounding /
+        seed, and no bit decision this step (scored groups re-decide bits on
+        update steps).  Storage is only replaced by steps that re-pack, by
+        ``load_state_dict`` and by ``add_param_group``, which all drop the cache.
+        """
+        sc = self.__dict__.get("_steady")
+        if sc is None or sc["state_obj"] is not self.state:
+            return None
+        if update_decision and any(g.get("bits") is None for g in self.param_groups):
+            return None
+        if sc["cfg"] != self._group_cfg():
+            return None
+        cur = [id(p) for g in self.param_groups for p in g["params"] if p.grad is not None]
+        if cur != sc["ids"]:
+            return None
+        return sc
+
+    def _steady_step(self, sc) -> bool:
+        """One step over the cached plans: ``step += 1`` per tensor, fresh grad
+        pointers, steps and per-group hyper-parameters; False (nothing launched,
+        nothing changed) if a grad no longer matches its plan."""
+        params, states = sc["params"], sc["states"]
+        t0 = time.perf_counter()
+        for plan, idx, _gidx in sc["runs"]:
+            if not plan.try_set_grads([params[i].grad for i in idx]):
+                return False
+        steps = []
+        for st in states:
+            st["step"] += 1
+            steps.append(st["step"])
+        steps = np.asarray(steps, np.int32)
+        groups = self.param_groups
+        lr = np.array([g["lr"] for g in groups], np.float32)
+        b1 = np.array([g["betas"][0] for g in groups], np.float32)
+        b2 = np.array([g["betas"][1] for g in groups], np.float32)
+        eps = np.array([g["eps"] for g in groups], np.float32)
+        wd = np.array([g["weight_decay"] for g in groups], np.float32)
+        unpack_ms = (time.perf_counter() - t0) * 1000.0
+        dev = params[0].device
+        prof = None
+        if self.sync_timing and self._kernel_profile_buf is not None and self._kernel_profile_device == dev:
+            prof = self._kernel_profile_buf
+        if self.sync_timing:
+            self._sync_device(dev)
+        tk0 = time.perf_counter()
+        for plan, idx, gidx in sc["runs"]:
+            a = plan.arr
+            a["step"] = steps[idx]
+            a["lr"] = lr[gidx]
+            a["beta1"] = b1[gidx]
+            a["beta2"] = b2[gidx]
+            a["eps"] = eps[gidx]
+            a["weight_decay"] = wd[gidx]
+            plan.run(prof)
+        if self.sync_timing:
+            self._sync_device(dev)
+        kernel_ms = (time.perf_counter() - tk0) * 1000.0
+        lt = self.last_step_timings
+        lt["quant_dequant_unpack_ms"] += unpack_ms
+        lt["quant_dequant_kernel_ms"] += kernel_ms
+        self._count_steady_params(len(states))
+        return True
+
+    def _count_steady_params(self, n: int) -> None:
+        """Per-tensor bookkeeping a steady step skips (FusedIO counts fast-path tensors)."""

@@ -1,18 +1,21 @@
 """Host logic of the drop-in optimizers on CPU tensors.
 
-The fused kernel needs a GPU, so these tests swap the kernel call
-(``_run_kernels``) for the CPU oracle on the same state tensors; everything
-else -- state init (stquant_opt_simple.py:212-225), the MDQ bit decision
+The fused kernel needs a GPU, so these tests swap the launch of each
+multi-tensor plan for the CPU oracle stepping every planned descriptor row on
+the same state tensors; everything else -- the bucketing and plan cache of
+``_run_kernels``, the steady-state path, state init (stquant_opt_simple.py:212-225), the MDQ bit decision
 (:93-109, :427-482), storage alignment / packing on bit changes (:114-210),
 FusedIO's fast path and double step increment (stquant_opt_fused_io.py:39-54),
 timing keys and state_dict -- runs as shipped.
 """
+import ctypes
 import io
 
 import numpy as np
 import pytest
 import torch
 
+import mdq_hip
 from oracle import mdq_oracle as orc
 from stquant_opt_fused_io import MDQAdamWSimpleFusedIO
 from stquant_opt_simple import MDQAdamWSimple
@@ -26,31 +29,47 @@ def _np(t):
     return t.numpy()
 
 
-def oracle_run_kernels(self, items):
-    for p, group in items:
-        st = self.state[p]
-        ea, easq = st["exp_avg"], st["exp_avg_sq"]
-        bits = int(st["current_bit"])
-        if bits == 4 and ea.dtype == torch.uint8 and easq.numel() == 0:
-            storage, cv = orc.STORE_P4, None
-        else:
-            storage = {torch.int8: orc.STORE_S8, torch.int16: orc.STORE_S16, torch.int32: orc.STORE_S32}[ea.dtype]
-            cv = _np(easq.view(-1))
-        b1, b2 = group["betas"]
-        orc.step(_np(p.data.view(-1)), _np(p.grad.view(-1)), _np(ea.view(-1)), cv,
-                 _np(st["scale_m"]), _np(st["scale_v"]), _np(st["v_min"]),
-                 beta1=b1, beta2=b2, lr=group["lr"], weight_decay=group["weight_decay"], eps=group["eps"],
-                 step=st["step"], bits=bits, block_size=min(int(group["block_size"]), 1024), storage=storage,
-                 rounding=0 if group.get("rounding", "nearest") == "nearest" else 1,
-                 seed=int(group.get("seed", 0)), tensor_id=self._tensor_ids.get(p, 0))
+_NP_DT = {0: np.float32, 1: np.uint16, 2: np.float16, 3: np.uint8, 4: np.int8, 5: np.int16,
+          6: np.uint16, 7: np.int32, 8: np.uint32}
+
+
+def _host_view(ptr, n, dt):
+    """numpy view of ``n`` elements at a CPU tensor's address (a planned descriptor pointer)."""
+    dt = np.dtype(dt)
+    if n == 0 or ptr == 0:
+        return np.zeros(0, dt)
+    return np.ctypeslib.as_array((ctypes.c_char * (n * dt.itemsize)).from_address(int(ptr))).view(dt)
+
+
+class OraclePlan(mdq_hip.MultiTensorPlan):
+    """The optimizer's real launch plan, executed row by row by the CPU oracle:
+    whatever the host code wrote into the ``stq_tensor`` descriptors (pointers,
+    sizes, steps, hyper-parameters, bits, tensor ids) is what gets stepped."""
+
+    def run(self, profile_cycles=None):
+        gdt, eadt, _ = self.codes
+        for r in self.arr:
+            n = int(r["numel"])
+            p4 = eadt == 3 and int(r["exp_avg_sq_numel"]) == 0
+            storage = orc.STORE_P4 if p4 else {4: orc.STORE_S8, 5: orc.STORE_S16, 7: orc.STORE_S32}[eadt]
+            dm, dv = orc.STORAGE_DTYPES[storage]
+            nb = int(r["scale_m_numel"])
+            orc.step(_host_view(r["p"], n, np.float32), _host_view(r["grad"], n, _NP_DT[gdt]),
+                     _host_view(r["exp_avg"], n, dm), None if p4 else _host_view(r["exp_avg_sq"], n, dv),
+                     _host_view(r["scale_m"], nb, np.float32), _host_view(r["scale_v"], nb, np.float32),
+                     _host_view(r["v_min"], nb, np.float32),
+                     beta1=float(r["beta1"]), beta2=float(r["beta2"]), lr=float(r["lr"]),
+                     weight_decay=float(r["weight_decay"]), eps=float(r["eps"]), step=int(r["step"]),
+                     bits=int(r["bits"]), block_size=self.block_size, storage=storage,
+                     rounding=self.rounding, seed=self.seed, tensor_id=int(r["tensor_id"]))
 
 
 class SimpleCPU(MDQAdamWSimple):
-    _run_kernels = oracle_run_kernels
+    _plan_cls = OraclePlan
 
 
 class FusedIOCPU(MDQAdamWSimpleFusedIO):
-    _run_kernels = oracle_run_kernels
+    _plan_cls = OraclePlan
 
 
 def make_params(shapes, seed=0):
@@ -220,3 +239,87 @@ def test_rejects_bad_options():
         MDQAdamWSimple(make_params([(4,)]), bits=5)
     with pytest.raises(ValueError):
         MDQAdamWSimple(make_params([(4,)]), rounding="up")
+
+
+class _CountSteady:
+    def _steady_step(self, sc):
+        ok = super()._steady_step(sc)
+        if ok:
+            self.__dict__.setdefault("steady_at", []).append(self.total_steps)
+        return ok
+
+
+class SimpleSteady(_CountSteady, SimpleCPU):
+    pass
+
+
+class FusedIOSteady(_CountSteady, FusedIOCPU):
+    pass
+
+
+class SimpleSlow(SimpleCPU):
+    def _steady_lookup(self, update_decision):
+        return None
+
+
+class FusedIOSlow(FusedIOCPU):
+    def _steady_lookup(self, update_decision):
+        return None
+
+
+def _same_state(oa, ob, pa, pb, tag):
+    for a, b in zip(pa, pb):
+        assert torch.equal(a.detach(), b.detach()), tag
+        sa, sb = oa.state[a], ob.state[b]
+        assert sa["step"] == sb["step"] and sa["current_bit"] == sb["current_bit"], tag
+        for k in ("exp_avg", "exp_avg_sq", "scale_m", "scale_v", "v_min"):
+            assert sa[k].dtype == sb[k].dtype and torch.equal(sa[k], sb[k]), (tag, k)
+
+
+@pytest.mark.parametrize("fast_cls,slow_cls", [(SimpleSteady, SimpleSlow), (FusedIOSteady, FusedIOSlow)])
+def test_steady_path_matches_slow_path(fast_cls, slow_cls):
+    """Reusing last step's plans (same tensors, storage, bits) gives byte-identical results
+    to rebuilding everything, through lr changes, a non-contiguous grad, a bit-width change,
+    a param without grad, scored bit decisions and a checkpoint reload."""
+    shapes = [(300, 7), (128,), (1000,), (5, 5)]
+    pa, pb = make_params(shapes, seed=4), make_params(shapes, seed=4)
+
+    def groups(ps):
+        return [{"params": ps[:2], "lr": 2e-3, "bits": 4}, {"params": ps[2:], "weight_decay": 0.0, "bits": 4}]
+    kw = dict(block_size=64, rounding="stochastic", seed=5, update_freq=3)
+    oa, ob = fast_cls(groups(pa), **kw), slow_cls(groups(pb), **kw)
+    for t in range(1, 19):
+        set_grads(pa, 50 + t)
+        set_grads(pb, 50 + t)
+        if t == 5:                                       # scheduler-style lr change
+            for o in (oa, ob):
+                o.param_groups[0]["lr"] = 5e-4
+        if t == 7:                                       # a non-contiguous grad
+            for ps in (pa, pb):
+                ps[0].grad = ps[0].grad.t().contiguous().t()
+        if t == 9:                                       # bit width change in one group
+            for o in (oa, ob):
+                o.param_groups[1]["bits"] = 8
+        if t == 11:                                      # one param without grad this step
+            pa[1].grad = None
+            pb[1].grad = None
+        if t == 13:                                      # scored bits from here on
+            for o in (oa, ob):
+                for g in o.param_groups:
+                    g["bits"] = None
+        if t == 16:                                      # checkpoint round trip
+            buf = io.BytesIO()
+            torch.save(oa.state_dict(), buf)
+            buf.seek(0)
+            oa.load_state_dict(torch.load(buf, weights_only=True))
+        oa.step()
+        ob.step()
+        _same_state(oa, ob, pa, pb, f"step {t}")
+        lt = oa.get_last_step_timings()
+        assert lt["mdq_fused_kernel_ms"] >= 0 and "mdq_quant_dequant_ms" in lt
+        if isinstance(oa, FusedIOSteady):
+            assert lt["mdq_fused_io_fast_path_params"] + lt["mdq_fused_io_fallback_params"] >= 3
+    # slow: 1-2 (first step re-packs int16 -> nibbles), 7 (non-contiguous grad), 9-10 (bits
+    # change re-packs), 11-12 (set of params with grads changes), 13 (group config changes),
+    # 15 and 18 (scored bit decisions), 16 (reload); steady everywhere else
+    assert oa.steady_at == [3, 4, 5, 6, 8, 14, 17], oa.steady_at
