@@ -255,6 +255,72 @@ def e2e_gpt2(steps: int, warmup: int, out_path):
     return res
 
 
+def bit_decision(steps: int):
+    """The MDQ bit decision of an update step (grad statistics + score -> bits), fused multi-tensor
+    kernel + one host read vs the reference's per-tensor torch reductions and per-tensor host
+    reads, on the GPT-2 small and LLaMA-7B tensor sets (timing keys of the optimizer)."""
+    import torch
+
+    from stquant_opt_simple import MDQAdamWSimple
+
+    dev = torch.device("cuda:0")
+    out = {}
+    for cfg in ("gpt2", "llama7b"):
+        shapes = CONFIGS[cfg][0]()
+        gdt = torch.bfloat16 if cfg == "llama7b" else torch.float32
+        params = []
+        for _, n in shapes:
+            p = torch.nn.Parameter(torch.empty(n, device=dev).normal_(0.0, 0.02))
+            if gdt != torch.float32:
+                p.grad_dtype = gdt                      # torch >= 2.10 checks .grad's dtype
+            p.grad = torch.empty(n, device=dev, dtype=gdt).normal_(0.0, 1e-3)
+            params.append(p)
+        res = {}
+        # the reference's score loop (stquant_opt_simple.py:446-466): 0-dim ops and one .item()
+        # host read per tensor, timed on the same stats as the vectorised loop
+        opt = MDQAdamWSimple(params, block_size=128, update_freq=1)
+        stats = MDQAdamWSimple._compute_grad_stats
+        st_t = torch.stack([stats(p.grad.float()) for p in params[:8]]).repeat(len(params) // 8 + 1, 1)[:len(params)]
+        opt.n_ema, opt.r_ema, opt.v_global_ema = st_t.mean(0).unbind(0)
+        tau = opt.param_groups[0]["tau"]
+        for rep in range(2):                            # the first pass loads the kernels
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for i in range(len(params)):
+                n_l, r_l, v_l = st_t[i]
+                s_t = 1.0 + (1.0 / torch.cosh(torch.tensor(7 / tau, device=dev, dtype=torch.float32)))
+                score = (7.2 + torch.log2(r_l / (opt.r_ema + 1e-12)) + torch.log2(n_l / (opt.n_ema + 1e-12))
+                         + torch.log2(s_t) + torch.log2(v_l / (opt.v_global_ema + 1e-12)))
+                MDQAdamWSimple._score_to_bits(score)
+            torch.cuda.synchronize()
+            res["reference_score_loop_ms"] = (time.perf_counter() - t0) * 1e3
+        for rep in range(2):
+            t0 = time.perf_counter()
+            opt._scores(st_t, [7] * len(params), tau).cpu().tolist()
+            torch.cuda.synchronize()
+            res["vectorised_score_ms"] = (time.perf_counter() - t0) * 1e3
+        log(f"bit decision {cfg}: score loop per tensor {res['reference_score_loop_ms']:.3f} ms, "
+            f"vectorised {res['vectorised_score_ms']:.3f} ms")
+        del opt
+        for mode in ("fused", "reference"):
+            opt = MDQAdamWSimple(params, block_size=128, update_freq=1, grad_stats=mode)
+            gs, sb = [], []
+            for t in range(steps + 1):
+                opt.step()
+                lt = opt.get_last_step_timings()
+                if t:
+                    gs.append(lt["mdq_grad_stats_ms"])
+                    sb.append(lt["mdq_score_bits_ms"])
+            res[mode] = {"grad_stats_ms": sum(gs) / len(gs), "score_bits_ms": sum(sb) / len(sb)}
+            log(f"bit decision {cfg} {mode}: grad stats {res[mode]['grad_stats_ms']:.3f} ms, "
+                f"score->bits {res[mode]['score_bits_ms']:.3f} ms")
+            del opt
+        out[cfg] = {"tensors": len(shapes), "params": sum(n for _, n in shapes), **res}
+        del params
+        torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(gdt: str, bits: int, B: int, seconds: float):
     """The oracle (C, OpenMP over quant blocks) on a 2^24-param slice of the same
     workload, repeated for about `seconds`; params/s over this host's cores."""
@@ -296,6 +362,8 @@ def main():
                     help="BASELINE config 3: GPT-2 small pretraining, stochastic vs nearest vs AdamW")
     ap.add_argument("--e2e-steps", type=int, default=300)
     ap.add_argument("--e2e-out", default=None, help="also write the loss histories as JSON here")
+    ap.add_argument("--bit-decision", action="store_true",
+                    help="time the update-step bit decision, fused vs the reference's per-tensor path")
     ap.add_argument("--copy-gib", type=float, default=0.0,
                     help="also run a plain device-to-device copy of this many GiB (rocprof calibration)")
     args = ap.parse_args()
@@ -312,6 +380,10 @@ def main():
         res = sweep_config5(dev, args.steps, args.warmup)
         print(json.dumps({"metric": "config 5 sweep: params/s and HBM GB/s per point", "n_gpus": 1,
                           "steps": args.steps, "warmup": args.warmup, "data": "synthetic", **res}), flush=True)
+        return
+    if args.bit_decision:
+        print(json.dumps({"metric": "MDQ bit decision per update step (ms)", "n_gpus": 1, "steps": args.steps,
+                          "data": "synthetic", "configs": bit_decision(args.steps)}), flush=True)
         return
     if args.e2e_gpt2:
         print(json.dumps(e2e_gpt2(args.e2e_steps, args.warmup, args.e2e_out)), flush=True)

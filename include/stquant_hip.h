@@ -124,6 +124,26 @@ int stq_multi_tensor_mdq_adamw(const stq_tensor *tensors, int n_tensors,
                                int64_t *profile_cycles, int64_t profile_numel,
                                void *stream);
 
+/*
+ * Per-tensor gradient statistics of the MDQ bit decision, for a whole tensor
+ * list: for tensor i with numel[i] elements of grad_dtype (STQ_FLOAT,
+ * STQ_BFLOAT16 or STQ_HALF) at grads[i],
+ *   stats[3i + 0] = sqrt(mean(g^2)),
+ *   stats[3i + 1] = std(g) / (mean(|g|) + 1e-12)   (std unbiased; NaN if numel == 1),
+ *   stats[3i + 2] = mean(g^2)                       (NaN means if numel == 0),
+ * into the device array stats[3 * n_tensors].  Sums are accumulated in fp64 in
+ * a fixed order (deterministic); the final divisions, square roots and the
+ * 1e-12 add are fp32, as the reference's.  Differs from the reference's fp32
+ * torch reductions by rounding only (about 1e-7 relative).  grads and numels
+ * are host arrays; the library keeps the descriptor table and the partial
+ * sums (24 bytes per 16384 elements) in its per-device ring.
+ *
+ * Replaces MDQAdamWSimple._compute_grad_stats called once per tensor
+ * (/root/reference/CUDA/stquant_opt_simple.py:93-98, loop at :427-431).
+ */
+int stq_multi_tensor_grad_stats(const void *const *grads, const int64_t *numels, int n_tensors,
+                                int grad_dtype, float *stats, void *stream);
+
 /* Last error message of this thread ("" when none). */
 const char *stq_last_error(void);
 

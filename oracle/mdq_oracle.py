@@ -25,6 +25,9 @@ v codes / scale_v      min-log element -> 0, max-log element -> 2^bits-1, tail l
 AdamW update           bits=32: matches a float64 textbook AdamW with v0 = e^-20 to
                        1e-6; lr=0 leaves p; g=0 state=0 gives p*(1-lr*wd) exactly
 stochastic rounding    unbiasedness and code histogram (tests/test_oracle_step.py)
+grad statistics        the reference's own torch expression (stquant_opt_simple.py:93-98)
+                       on CPU tensors, closed forms for constant / two-valued grads,
+                       numel 0 / 1 NaN cases (tests/test_oracle_grad_stats.py)
 =====================  ==============================================================
 
 Parity with the CUDA binary itself is unpinned at one boundary only: the ulp-level
@@ -207,3 +210,21 @@ def init_state(n: int, block_size: int, storage: int):
         code_v = np.zeros(n, dtype=dv)
     return (code_m, code_v, np.zeros(nb, np.float32), np.zeros(nb, np.float32),
             np.full(nb, -20.0, np.float32))
+
+
+def grad_stats(g: np.ndarray) -> np.ndarray:
+    """``stquant_opt_simple.py:93-98`` restated for one gradient: float32
+    ``[sqrt(mean(g^2)), std(g) / (mean(|g|) + 1e-12), mean(g^2)]`` with the
+    unbiased std, sums in float64 (two-pass variance), then the reference's
+    final fp32 operations (sqrt of the fp32 mean, fp32 divide and add).
+    numel 0 gives NaN means; numel 1 a NaN std, as torch does."""
+    x = np.asarray(g, dtype=np.float64).ravel()
+    n = x.size
+    nan = np.float32(np.nan)
+    with np.errstate(all="ignore"):
+        mean_sq = np.float32(np.sum(x * x) / n) if n else nan
+        mean_abs = np.float32(np.sum(np.abs(x)) / n) if n else nan
+        sd = np.float32(np.sqrt(np.var(x, ddof=1))) if n > 1 else nan
+        n_l = np.sqrt(mean_sq, dtype=np.float32)
+        r_l = np.float32(sd / np.float32(mean_abs + np.float32(1e-12)))
+    return np.array([n_l, r_l, mean_sq], dtype=np.float32)

@@ -19,6 +19,7 @@
 #include "mdq_desc.h"
 #include "mdq_launch.h"
 #include "mdq_math.h"
+#include "mdq_stats.h"
 
 namespace {
 
@@ -193,16 +194,11 @@ int get_ctx(DevCtx **out)
     return STQ_OK;
 }
 
-// Uploads descs to a device slot on `stream` and launches.  The slot's pinned
-// staging buffer is reused only after the event recorded behind its previous
-// launch has completed.
-int upload_and_launch(const std::vector<MdqDesc> &descs, int storage, int grad_dt, int log2b, bool sr,
-                      int64_t total_tiles, unsigned long long *prof, uint64_t seed, hipStream_t stream)
+// The next slot of the device's ring with at least `need` device bytes (and
+// as many pinned staging bytes), after the work recorded behind its previous
+// use has completed.  Called with ctx->mu held.
+int take_slot(DevCtx *ctx, size_t need, Slot **out)
 {
-    DevCtx *ctx = nullptr;
-    int rc = get_ctx(&ctx);
-    if (rc != STQ_OK) return rc;
-    std::lock_guard<std::mutex> lk(ctx->mu);
     Slot &s = ctx->slots[ctx->next];
     ctx->next = (ctx->next + 1) % 8;
     hipError_t e;
@@ -211,8 +207,6 @@ int upload_and_launch(const std::vector<MdqDesc> &descs, int storage, int grad_d
         if (e != hipSuccess) return hip_fail(e, "hipEventSynchronize");
         s.pending = false;
     }
-    const size_t n = descs.size();
-    const size_t need = n * (sizeof(MdqDesc) + sizeof(long long));
     if (s.cap < need) {
         if (s.dev) { (void)hipFree(s.dev); s.dev = nullptr; }
         if (s.host) { (void)hipHostFree(s.host); s.host = nullptr; }
@@ -228,10 +222,39 @@ int upload_and_launch(const std::vector<MdqDesc> &descs, int storage, int grad_d
         e = hipEventCreateWithFlags(&s.done, hipEventDisableTiming);
         if (e != hipSuccess) return hip_fail(e, "hipEventCreate");
     }
+    *out = &s;
+    return STQ_OK;
+}
+
+// Marks the slot busy until the work queued so far on `stream` completes.
+int release_slot(Slot *s, hipStream_t stream)
+{
+    hipError_t e = hipEventRecord(s->done, stream);
+    if (e != hipSuccess) return hip_fail(e, "hipEventRecord");
+    s->pending = true;
+    return STQ_OK;
+}
+
+// Uploads descs to a device slot on `stream` and launches.  The slot's pinned
+// staging buffer is reused only after the event recorded behind its previous
+// launch has completed.
+int upload_and_launch(const std::vector<MdqDesc> &descs, int storage, int grad_dt, int log2b, bool sr,
+                      int64_t total_tiles, unsigned long long *prof, uint64_t seed, hipStream_t stream)
+{
+    DevCtx *ctx = nullptr;
+    int rc = get_ctx(&ctx);
+    if (rc != STQ_OK) return rc;
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    const size_t n = descs.size();
+    const size_t need = n * (sizeof(MdqDesc) + sizeof(long long));
+    Slot *sp = nullptr;
+    rc = take_slot(ctx, need, &sp);
+    if (rc != STQ_OK) return rc;
+    Slot &s = *sp;
     std::memcpy(s.host, descs.data(), n * sizeof(MdqDesc));
     long long *tb = reinterpret_cast<long long *>(s.host + n * sizeof(MdqDesc));
     for (size_t i = 0; i < n; ++i) tb[i] = descs[i].tile_begin;
-    e = hipMemcpyAsync(s.dev, s.host, need, hipMemcpyHostToDevice, stream);
+    hipError_t e = hipMemcpyAsync(s.dev, s.host, need, hipMemcpyHostToDevice, stream);
     if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(descriptors)");
 
     const MdqDesc *dd = reinterpret_cast<const MdqDesc *>(s.dev);
@@ -244,10 +267,53 @@ int upload_and_launch(const std::vector<MdqDesc> &descs, int storage, int grad_d
     default: e = mdq::launch_s32(dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream); break;
     }
     if (e != hipSuccess) return hip_fail(e, "kernel launch");
-    e = hipEventRecord(s.done, stream);
-    if (e != hipSuccess) return hip_fail(e, "hipEventRecord");
-    s.pending = true;
-    return STQ_OK;
+    return release_slot(&s, stream);
+}
+
+// stq_multi_tensor_grad_stats: descriptors, tile starts and the fp64 partial
+// sums share one ring slot.
+int run_grad_stats(const void *const *grads, const int64_t *numels, int n, int grad_dt, float *stats,
+                   hipStream_t stream)
+{
+    g_err.clear();
+    if (grad_dt != STQ_FLOAT && grad_dt != STQ_BFLOAT16 && grad_dt != STQ_HALF)
+        return fail(STQ_ERR_INVALID, "grad must be Float, BFloat16 or Half, got %s", dtype_name(grad_dt));
+    if (n < 0 || (n > 0 && (!grads || !numels || !stats)))
+        return fail(STQ_ERR_INVALID, "grad_stats: bad tensor list or output");
+    if (n == 0) return STQ_OK;
+    std::vector<mdq::StatDesc> d((size_t)n);
+    int64_t tiles = 0;
+    for (int i = 0; i < n; ++i) {
+        if (numels[i] < 0) return fail(STQ_ERR_INVALID, "tensor %d: negative numel", i);
+        if (numels[i] > 0 && !grads[i]) return fail(STQ_ERR_INVALID, "tensor %d: null grad", i);
+        d[i].g = grads[i];
+        d[i].numel = numels[i];
+        d[i].tile_begin = tiles;
+        tiles += (numels[i] + mdq::STAT_TILE - 1) / mdq::STAT_TILE;
+        d[i].tile_end = tiles;
+    }
+    if (tiles > 0x7fffffffLL)
+        return fail(STQ_ERR_INVALID, "too many tiles in one call (%lld); split the tensor list", (long long)tiles);
+    DevCtx *ctx = nullptr;
+    int rc = get_ctx(&ctx);
+    if (rc != STQ_OK) return rc;
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    const size_t up = (size_t)n * (sizeof(mdq::StatDesc) + sizeof(long long));
+    const size_t part_off = (up + 255) / 256 * 256;
+    Slot *s = nullptr;
+    rc = take_slot(ctx, part_off + (size_t)tiles * 3 * sizeof(double), &s);
+    if (rc != STQ_OK) return rc;
+    std::memcpy(s->host, d.data(), (size_t)n * sizeof(mdq::StatDesc));
+    long long *tb = reinterpret_cast<long long *>(s->host + (size_t)n * sizeof(mdq::StatDesc));
+    for (int i = 0; i < n; ++i) tb[i] = d[i].tile_begin;
+    hipError_t e = hipMemcpyAsync(s->dev, s->host, up, hipMemcpyHostToDevice, stream);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(descriptors)");
+    const mdq::StatDesc *dd = reinterpret_cast<const mdq::StatDesc *>(s->dev);
+    const long long *dtb = reinterpret_cast<const long long *>(s->dev + (size_t)n * sizeof(mdq::StatDesc));
+    double *partials = reinterpret_cast<double *>(s->dev + part_off);
+    e = mdq::launch_grad_stats(dd, dtb, n, tiles, grad_dt, partials, stats, stream);
+    if (e != hipSuccess) return hip_fail(e, "grad_stats launch");
+    return release_slot(s, stream);
 }
 
 int common_checks(int grad_dt, int block_size, int rounding, const int64_t *prof, int64_t prof_numel,
@@ -357,6 +423,12 @@ int stq_multi_tensor_mdq_adamw(const stq_tensor *tensors, int n_tensors, int gra
 {
     return run(tensors, n_tensors, grad_dtype, exp_avg_dtype, exp_avg_sq_dtype, block_size, rounding, seed,
                profile_cycles, profile_numel, stream);
+}
+
+int stq_multi_tensor_grad_stats(const void *const *grads, const int64_t *numels, int n_tensors,
+                                int grad_dtype, float *stats, void *stream)
+{
+    return run_grad_stats(grads, numels, n_tensors, grad_dtype, stats, reinterpret_cast<hipStream_t>(stream));
 }
 
 const char *stq_last_error(void) { return g_err.c_str(); }

@@ -240,6 +240,42 @@ def multi_tensor_step(entries: Sequence[TensorState], block_size: int, *,
     MultiTensorPlan(entries, block_size, rounding=rounding, seed=seed).run(profile_cycles)
 
 
+def grad_stats(grads: Sequence[torch.Tensor], out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Per-tensor ``(sqrt(mean g^2), std(g) / (mean|g| + 1e-12), mean g^2)`` as a float32
+    ``[len(grads), 3]`` device tensor, from one multi-tensor launch per grad dtype (fp64 sums,
+    fixed order).  The reference computes the same three values per tensor with fp32 torch
+    reductions (stquant_opt_simple.py:93-98)."""
+    n = len(grads)
+    if n == 0:
+        return torch.empty(0, 3, dtype=torch.float32)
+    dev = grads[0].device
+    if dev.type != "cuda":
+        raise RuntimeError("grad_stats: grads must be CUDA tensors")
+    if out is None:
+        out = torch.empty(n, 3, dtype=torch.float32, device=dev)
+    elif out.shape != (n, 3) or out.dtype != torch.float32 or out.device != dev or not out.is_contiguous():
+        raise RuntimeError("grad_stats: out must be a contiguous float32 [n, 3] tensor on the grads' device")
+    by_dtype = {}
+    for i, g in enumerate(grads):
+        if g.device != dev:
+            raise RuntimeError("grad_stats: all grads must be on one device")
+        by_dtype.setdefault(g.dtype, []).append(i)
+    keep = []
+    with torch.cuda.device(dev):
+        stream = _capi.stream_handle(dev)
+        for dt, idx in by_dtype.items():
+            gs = [grads[i] if grads[i].is_contiguous() else grads[i].contiguous() for i in idx]
+            keep.extend(gs)
+            ptrs = np.array([g.data_ptr() if g.numel() else 0 for g in gs], dtype=np.uint64)
+            numels = np.array([g.numel() for g in gs], dtype=np.int64)
+            dst = out if len(idx) == n else torch.empty(len(idx), 3, dtype=torch.float32, device=dev)
+            check(lib().stq_multi_tensor_grad_stats(ptrs.ctypes.data, numels.ctypes.data, len(idx),
+                                                    dtype_code(dt), dst.data_ptr(), stream))
+            if dst is not out:
+                out[torch.as_tensor(idx, device=dev)] = dst
+    return out
+
+
 def device_math(which: str, x: torch.Tensor) -> torch.Tensor:
     """Device e^x (``which='exp'``) or log x (``'log'``) with the kernels' own fp32 code."""
     assert x.is_cuda and x.dtype == torch.float32 and x.is_contiguous()

@@ -51,12 +51,15 @@ class MDQAdamWSimple(Optimizer):
         rounding="nearest",
         seed=0,
         sync_timing=True,
+        grad_stats="fused",
     ):
         # stquant_opt_simple.py:33-44
         tau_adaptive = 300 * math.log(layer_count) * math.sqrt(batch_size)
         if bits is not None and int(bits) not in (4, 8, 16, 32):
             raise ValueError(f"bits must be one of 4, 8, 16, 32 or None, got {bits}")
         mdq_hip.rounding_code(rounding)
+        if grad_stats not in ("fused", "reference"):
+            raise ValueError(f"grad_stats must be 'fused' or 'reference', got {grad_stats!r}")
         defaults = dict(
             lr=lr,
             betas=betas,
@@ -78,6 +81,7 @@ class MDQAdamWSimple(Optimizer):
         self.total_steps = 0
         self.last_step_timings = {}
         self.sync_timing = sync_timing
+        self.grad_stats = grad_stats
         self._kernel_profile_buf = None
         self._kernel_profile_device = None
 
@@ -128,6 +132,27 @@ class MDQAdamWSimple(Optimizer):
         r_l = torch.std(grad) / (grad.abs().mean() + 1e-12)
         v_l = torch.mean(grad * grad)
         return torch.stack([n_l, r_l, v_l])
+
+    def _all_grad_stats(self, grads):
+        """``[n, 3]`` stats of all grads: one fused launch per grad dtype, or the reference's
+        per-tensor torch reductions (``grad_stats="reference"``, stquant_opt_simple.py:427-431)."""
+        if self.grad_stats == "fused" and grads and grads[0].is_cuda:
+            return mdq_hip.grad_stats(grads)
+        return torch.stack([self._compute_grad_stats(g.float()) for g in grads])
+
+    def _scores(self, stats_tensor, steps, tau):
+        """The reference's per-tensor score (stquant_opt_simple.py:446-466) for all tensors at
+        once: the same fp32 torch expressions, element for element, on ``[n]`` vectors."""
+        n_l, r_l, v_l = stats_tensor[:, 0], stats_tensor[:, 1], stats_tensor[:, 2]
+        t = torch.tensor([s / tau for s in steps], device=stats_tensor.device, dtype=torch.float32)
+        s_t = 1.0 + (1.0 / torch.cosh(t))
+        return (
+            7.2
+            + torch.log2(r_l / (self.r_ema + 1e-12))
+            + torch.log2(n_l / (self.n_ema + 1e-12))
+            + torch.log2(s_t)
+            + torch.log2(v_l / (self.v_global_ema + 1e-12))
+        )
 
     @staticmethod
     def _score_to_bits(score) -> int:
@@ -569,7 +594,6 @@ class MDQAdamWSimple(Optimizer):
         self._steady = None
 
         params_with_grad = []
-        all_stats = []
 
         for group in self.param_groups:
             b_size = min(int(group.get("block_size", 256)), 1024)
@@ -590,18 +614,17 @@ class MDQAdamWSimple(Optimizer):
         allreduce_ms = 0.0
         score_bits_ms = 0.0
 
+        stats_tensor = None
         if update_decision and params_with_grad and scored:
             dev = params_with_grad[0][0].device
             self._sync_device(dev)
             t_grad = time.perf_counter()
-            for p, _group in params_with_grad:
-                all_stats.append(self._compute_grad_stats(p.grad.float()))
+            stats_tensor = self._all_grad_stats([p.grad for p, _g in params_with_grad])
             self._sync_device(dev)
             grad_stats_ms = (time.perf_counter() - t_grad) * 1000.0
 
-        if update_decision and all_stats:
+        if stats_tensor is not None:
             dev = params_with_grad[0][0].device
-            stats_tensor = torch.stack(all_stats)
             avg_stats = stats_tensor.mean(dim=0)
 
             if dist.is_available() and dist.is_initialized():
@@ -625,21 +648,12 @@ class MDQAdamWSimple(Optimizer):
                 self.v_global_ema = alpha * avg_stats[2] + (1 - alpha) * self.v_global_ema
 
             tau = self.param_groups[0]["tau"]
-            for i, (p, _group) in enumerate(params_with_grad):
-                state = self.state[p]
-                n_l, r_l, v_l = stats_tensor[i]
-                s_t = 1.0 + (
-                    1.0 / torch.cosh(torch.tensor(state["step"] / tau, device=p.device, dtype=torch.float32))
-                )
-                score = (
-                    7.2
-                    + torch.log2(r_l / (self.r_ema + 1e-12))
-                    + torch.log2(n_l / (self.n_ema + 1e-12))
-                    + torch.log2(s_t)
-                    + torch.log2(v_l / (self.v_global_ema + 1e-12))
-                )
-                state["last_score"] = score
-                state["current_bit"] = self._score_to_bits(score)
+            states = [self.state[p] for p, _g in params_with_grad]
+            scores = self._scores(stats_tensor, [st["step"] for st in states], tau)
+            host_scores = scores.cpu().tolist()          # the step's one device -> host read
+            for st, sc, hs in zip(states, scores.unbind(0), host_scores):
+                st["last_score"] = sc
+                st["current_bit"] = self._score_to_bits(hs)
             self._sync_device(dev)
             score_bits_ms = (time.perf_counter() - t_score) * 1000.0
 
