@@ -110,12 +110,16 @@ def bytes_per_param(grad_bytes: int, bits: int, block: int) -> float:
     return 8 + grad_bytes + 2 * code + 24.0 / block
 
 
-def build_workload(name, dev, seed=0):
+STORAGE_NAMES = {4: "p4", 8: "s8", 16: "s16", 32: "s32"}
+
+
+def build_workload(name, dev, seed=0, bits=None):
     import torch
 
     import mdq_hip
 
-    shapes_fn, gdt, bits, B = CONFIGS[name]
+    shapes_fn, gdt, cfg_bits, B = CONFIGS[name]
+    bits = cfg_bits if bits is None else bits
     shapes = shapes_fn()
     sizes = [n for _, n in shapes]
     N = sum(sizes)
@@ -131,7 +135,14 @@ def build_workload(name, dev, seed=0):
         k = min(chunk, N - o)
         p[o:o + k].normal_(0.0, 0.02, generator=gen)
         g[o:o + k].copy_(torch.randn(k, device=dev, generator=gen).mul_(1e-3))
-    codes = torch.full((N,), 0x08, dtype=torch.uint8, device=dev)   # m code 0, v code 0
+    if bits == 4:
+        codes = torch.full((N,), 0x08, dtype=torch.uint8, device=dev)   # m code 0, v code 0
+        vcodes = None
+    else:
+        mdt, vdt = {8: (torch.int8, torch.uint8), 16: (torch.int16, torch.uint16),
+                    32: (torch.int32, torch.uint32)}[bits]
+        codes = torch.zeros(N, dtype=mdt, device=dev)
+        vcodes = torch.zeros(N, dtype=vdt, device=dev)
     sm = torch.zeros(NB, dtype=torch.float32, device=dev)
     sv = torch.zeros(NB, dtype=torch.float32, device=dev)
     vm = torch.full((NB,), -20.0, dtype=torch.float32, device=dev)
@@ -140,13 +151,14 @@ def build_workload(name, dev, seed=0):
     o = ob = 0
     for i, (n, nb) in enumerate(zip(sizes, nbs)):
         entries.append(mdq_hip.TensorState(
-            p[o:o + n], g[o:o + n], codes[o:o + n], empty, sm[ob:ob + nb], sv[ob:ob + nb], vm[ob:ob + nb],
+            p[o:o + n], g[o:o + n], codes[o:o + n], empty if vcodes is None else vcodes[o:o + n],
+            sm[ob:ob + nb], sv[ob:ob + nb], vm[ob:ob + nb],
             1, bits, 1e-3, 0.9, 0.999, 1e-8, 0.01, i))
         o += n
         ob += nb
     plan = mdq_hip.MultiTensorPlan(entries, B)
     return dict(plan=plan, N=N, tensors=len(sizes), B=B, bits=bits, gdt=gdt,
-                grad_bytes=2 if gdt == "bf16" else 4, keep=(p, g, codes, sm, sv, vm))
+                grad_bytes=2 if gdt == "bf16" else 4, keep=(p, g, codes, vcodes, sm, sv, vm))
 
 
 ALIGN_ELEMS = 256
@@ -333,18 +345,19 @@ def cpu_baseline(gdt: str, bits: int, B: int, seconds: float):
     p = (rng.standard_normal(n) * 0.02).astype(np.float32)
     g32 = (rng.standard_normal(n) * 1e-3).astype(np.float32)
     g = (g32.view(np.uint32) >> 16).astype(np.uint16) if gdt == "bf16" else g32
-    cm, cv, sm, sv, vm = orc.init_state(n, B, orc.STORE_P4)
+    storage = {4: orc.STORE_P4, 8: orc.STORE_S8, 16: orc.STORE_S16, 32: orc.STORE_S32}[bits]
+    cm, cv, sm, sv, vm = orc.init_state(n, B, storage)
     cores = len(os.sched_getaffinity(0))
     steps, t0 = 0, time.perf_counter()
     while True:
         orc.step(p, g, cm, cv, sm, sv, vm, beta1=0.9, beta2=0.999, lr=1e-3, weight_decay=0.01, eps=1e-8,
-                 step=steps + 1, bits=bits, block_size=B, storage=orc.STORE_P4, threads=cores)
+                 step=steps + 1, bits=bits, block_size=B, storage=storage, threads=cores)
         steps += 1
         el = time.perf_counter() - t0
         if el >= seconds:
             break
     return dict(value=n * steps / el, unit="params/s", cores=cores, kind="port",
-                sample=f"{n} params ({gdt} grads, {bits}-bit packed, B={B}) x {steps} steps, "
+                sample=f"{n} params ({gdt} grads, {bits}-bit codes, B={B}) x {steps} steps, "
                        f"{el:.1f} s, oracle/mdq_oracle.c with {cores} OpenMP threads")
 
 
@@ -355,6 +368,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="llama7b", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--bits", type=int, default=None, choices=(4, 8, 16, 32),
+                    help="code width (canonical storage: packed nibbles, int8/16/32 + uint8/16/32); "
+                         "default: the config's (4)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--sweep-config5", action="store_true",
                     help="time BASELINE config 5 over bits x block x rounding (one JSON line with all points)")
@@ -388,7 +404,7 @@ def main():
     if args.e2e_gpt2:
         print(json.dumps(e2e_gpt2(args.e2e_steps, args.warmup, args.e2e_out)), flush=True)
         return
-    w = build_workload(args.config, dev)
+    w = build_workload(args.config, dev, bits=args.bits)
     plan = w["plan"]
     torch.cuda.synchronize()
 
@@ -436,7 +452,7 @@ def main():
     # HBM bytes per launch measured by rocprofv3 (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0,
     # the factors that map a plain 4 GiB copy's counters to 4 GiB), committed under profiles/
     traffic, traffic_src = None, None
-    prof_json = os.path.join(ROOT, "profiles", f"mdq_step_{args.config}_{w['gdt']}_p4_b{w['B']}.json")
+    prof_json = os.path.join(ROOT, "profiles", f"mdq_step_{args.config}_{w['gdt']}_{STORAGE_NAMES[w['bits']]}_b{w['B']}.json")
     if os.path.exists(prof_json):
         with open(prof_json) as f:
             traffic = json.load(f)["traffic_bytes"]
@@ -463,7 +479,8 @@ def main():
         "data": "synthetic",
         "config": {
             "workload": f"{args.config}: {w['tensors']} tensors, {N} fp32 params, {w['gdt']} grads, "
-                        f"{w['bits']}-bit packed m/v, block {w['B']}, nearest rounding, one multi-tensor launch",
+                        f"{w['bits']}-bit {'packed ' if w['bits'] == 4 else ''}m/v codes, block {w['B']}, "
+                        f"nearest rounding, one multi-tensor launch",
             "params": N,
             "tensors": w["tensors"],
             "block_size": w["B"],

@@ -163,6 +163,15 @@ int stq_device_math(int which, const float *x, float *y, int64_t n, void *stream
 int stq_device_math_digests(int which, uint32_t first, uint32_t count, uint32_t chunk,
                             uint64_t *digests, void *stream);
 
+/*
+ * max over the floats with bit patterns first .. first+count-1 (positive and
+ * finite) of |v_log_f32(x) * ln 2 - (the kernels' log x)|, computed in fp64 and
+ * atomically max-ed, as the bit pattern of a double, into the device uint64
+ * *max_err_bits (zeroed by the caller).  The step kernel's fast v-code path
+ * relies on this bound (no reference counterpart).
+ */
+int stq_device_log_approx_error(uint32_t first, uint32_t count, uint64_t *max_err_bits, void *stream);
+
 /* Host (CPU) builds of the same inline functions the kernels use. */
 void stq_host_math(int which, const float *x, float *y, int64_t n);
 /* out[i] = round-half-away(u[i] / d[i]) via the kernel's fp32 fma method,

@@ -444,6 +444,16 @@ int stq_device_math(int which, const float *x, float *y, int64_t n, void *stream
     return e == hipSuccess ? STQ_OK : hip_fail(e, "math kernel launch");
 }
 
+int stq_device_log_approx_error(uint32_t first, uint32_t count, uint64_t *max_err_bits, void *stream)
+{
+    g_err.clear();
+    if ((uint64_t)first + count > 0x100000000ull) return fail(STQ_ERR_INVALID, "range exceeds 2^32");
+    if (count > 0 && !max_err_bits) return fail(STQ_ERR_INVALID, "null output");
+    hipError_t e = mdq::launch_log_approx_err(first, count, reinterpret_cast<unsigned long long *>(max_err_bits),
+                                              reinterpret_cast<hipStream_t>(stream));
+    return e == hipSuccess ? STQ_OK : hip_fail(e, "log error kernel launch");
+}
+
 int stq_device_math_digests(int which, uint32_t first, uint32_t count, uint32_t chunk, uint64_t *digests,
                             void *stream)
 {

@@ -27,6 +27,11 @@
 
 namespace mdq {
 
+// Bound on |v_log_f32(x) * ln 2 - mdq_logf(x)| over every float x in
+// [1e-12, FLT_MAX]: measured 9.114e-6 on gfx950 (stq_device_log_approx_error,
+// all inputs); the kernel uses 1.75 times that.
+#define MDQ_LOG_APPROX_ERR 1.6e-5f
+
 template <int LOG2B>
 struct Cfg {
     static constexpr int B = 1 << LOG2B;
@@ -413,18 +418,58 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
     }
     if (prof_on) { unsigned long long t = clock64(); pa.c[1] += t - t0; t0 = t; }
 
+    // Fast v-code path: nearest rounding, code width <= 8 bits, a one-wave
+    // tile with every element inside the tensor and every x = v + 1e-12 a
+    // finite float >= 1e-12 (wave-uniform).  log is non-decreasing on that
+    // range (checked for every float), so the block's max / min of log x are
+    // the logs of its max / min x: two exact logs per lane instead of one per
+    // element.  The per-element v codes then come from the hardware log (see
+    // the requant below).
+    constexpr bool FAST_OK = FULL && !SR && C::WAVES == 1;
+    bool fastv = false;
+    if constexpr (FAST_OK) {
+        if (d.bits <= 8u) {
+            bool good = true;
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) {
+                const float x = v[e] + 1e-12f;
+                good = good && x >= 1e-12f && x <= __FLT_MAX__;
+            }
+            fastv = __builtin_amdgcn_ballot_w64(!good) == 0;
+        }
+    }
+
     // |m|, log(v + 1e-12) and the three block reductions (:92-97); lanes
     // outside the tensor contribute 0 to all three.
     float amax = 0.0f, lmax = 0.0f, lmin = 0.0f;
+    int32_t ka, kx, kn;
+    if (fastv) {
+        float xmax = 0.0f, xmin = 0.0f;
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-        const float a = ok[e] ? fabsf(m[e]) : 0.0f;
-        const float l = ok[e] ? mdq_logf(v[e] + 1e-12f) : 0.0f;
-        lv[e] = l;
-        if (e == 0) { amax = a; lmax = l; lmin = l; }
-        else { amax = fmaxf(amax, a); lmax = fmaxf(lmax, l); lmin = fminf(lmin, l); }
+        for (int e = 0; e < EPL; ++e) {
+            const float a = fabsf(m[e]);
+            const float x = v[e] + 1e-12f;
+            amax = e == 0 ? a : fmaxf(amax, a);
+            xmax = e == 0 ? x : fmaxf(xmax, x);
+            xmin = e == 0 ? x : fminf(xmin, x);
+        }
+        // positive finite floats order as their int32 bit patterns
+        ka = __builtin_bit_cast(int32_t, amax);
+        kx = __builtin_bit_cast(int32_t, xmax);
+        kn = __builtin_bit_cast(int32_t, xmin);
+    } else {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+            const float a = ok[e] ? fabsf(m[e]) : 0.0f;
+            const float l = ok[e] ? mdq_logf(v[e] + 1e-12f) : 0.0f;
+            lv[e] = l;
+            if (e == 0) { amax = a; lmax = l; lmin = l; }
+            else { amax = fmaxf(amax, a); lmax = fmaxf(lmax, l); lmin = fminf(lmin, l); }
+        }
+        ka = __builtin_bit_cast(int32_t, amax);
+        kx = f2key(lmax);
+        kn = f2key(lmin);
     }
-    int32_t ka = __builtin_bit_cast(int32_t, amax), kx = f2key(lmax), kn = f2key(lmin);
     if constexpr (LPB <= 64) {
         ka = group_reduce<LPB, true>(ka);
         kx = group_reduce<LPB, true>(kx);
@@ -441,8 +486,22 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
         kn = iop<false>(kn, xw[o + 2]);
     }
     amax = __builtin_bit_cast(float, ka);
-    lmax = key2f(kx);
-    lmin = key2f(kn);
+    if (fastv) {
+        if constexpr (LPB >= 2) {
+            // one exact log per lane: even lanes log(xmax), odd lanes log(xmin),
+            // then each lane takes both from its lane pair (quad_perm DPP)
+            const int32_t ks = (lane & 1) ? kn : kx;
+            const int32_t ls = __builtin_bit_cast(int32_t, mdq_logf(__builtin_bit_cast(float, ks)));
+            lmax = __builtin_bit_cast(float, dpp_i<0xA0>(ls));   // quad_perm [0,0,2,2]
+            lmin = __builtin_bit_cast(float, dpp_i<0xF5>(ls));   // quad_perm [1,1,3,3]
+        } else {
+            lmax = mdq_logf(__builtin_bit_cast(float, kx));
+            lmin = mdq_logf(__builtin_bit_cast(float, kn));
+        }
+    } else {
+        lmax = key2f(kx);
+        lmin = key2f(kn);
+    }
 
     // new scales (:101-106)
     const float s_sm = (amax + 1e-12f) * d.inv_qm;            // == / 2^(bits-1), exact
@@ -504,11 +563,47 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
             const float hdm = 0.5f * dm, hdv = 0.5f * dv;
             const float ilm = mdq_inv_lo(__builtin_amdgcn_rcpf(dm));
             const float ilv = mdq_inv_lo(__builtin_amdgcn_rcpf(dv));
+            if (fastv) {
+                // The exact code is K = round-half-away(u / dv), u = fl(log x - vmin).
+                // z = fl(log2_hw(x) * c1 + c0) with c1 = ln2 / dv and c0 = -vmin / dv, each
+                // from one hardware reciprocal r (up to 4 ulp off: c1, c0 within 1.25 * 2^-21
+                // relative), differs from u / dv by at most
+                // E = (A + 1.3e-6 L) / dv + (QV + 1) 2^-24, where A bounds
+                // |log2_hw(x) ln 2 - log x| over every float x >= 1e-12 (MDQ_LOG_APPROX_ERR,
+                // measured exhaustively on the device) and L = max(|lmax|, |lmin|).  Where z is
+                // farther than E + 2^-16 from a half-integer, floor(z + 1/2) is K (the 2^-16
+                // covers the rounding of z + 1/2 below 512); the other elements take the exact
+                // path.
+                const float r = __builtin_amdgcn_rcpf(dv);
+                const float c1 = 0.69314718f * r;
+                const float c0 = -s_vmin * r;
+                const float L = fmaxf(fabsf(lmax), fabsf(lmin));
+                const float ep = (fma_(L, 1.3e-6f, MDQ_LOG_APPROX_ERR) * r + fma_(d.qvf, 6.0e-8f, 1.6e-5f)) * 1.001f;
+                const float near = 0.5f - ep;
+                bool redo[EPL];
+                bool any = false;
 #pragma unroll
-            for (int e = 0; e < EPL; ++e) {
-                const float K = mdq_round_half_away(fabsf(m[e]), dm, ilm, hdm);
-                qmf[e] = __builtin_copysignf(K, m[e]);
-                qvf[e] = mdq_round_half_away(lv[e] - s_vmin, dv, ilv, hdv);
+                for (int e = 0; e < EPL; ++e) {
+                    const float K = mdq_round_half_away(fabsf(m[e]), dm, ilm, hdm);
+                    qmf[e] = __builtin_copysignf(K, m[e]);
+                    const float z = fma_(__builtin_amdgcn_logf(v[e] + 1e-12f), c1, c0);
+                    const float kv = floor_(z + 0.5f);
+                    qvf[e] = kv;
+                    redo[e] = fabsf(z - kv) >= near;
+                    any = any || redo[e];
+                }
+                if (__builtin_amdgcn_ballot_w64(any)) {
+#pragma unroll
+                    for (int e = 0; e < EPL; ++e)
+                        if (redo[e]) qvf[e] = mdq_round_half_away(mdq_logf(v[e] + 1e-12f) - s_vmin, dv, ilv, hdv);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) {
+                    const float K = mdq_round_half_away(fabsf(m[e]), dm, ilm, hdm);
+                    qmf[e] = __builtin_copysignf(K, m[e]);
+                    qvf[e] = mdq_round_half_away(lv[e] - s_vmin, dv, ilv, hdv);
+                }
             }
         }
 #pragma unroll

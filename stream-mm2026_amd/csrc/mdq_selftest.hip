@@ -47,6 +47,35 @@ __global__ __launch_bounds__(256) void math_digest_kernel(int which, unsigned fi
     }
 }
 
+// max over x = bits_f(first .. first+count-1) of |log2_hw(x) * ln 2 - mdq_logf(x)| in fp64,
+// as the bit pattern of a non-negative double (atomic max over uint64 orders those).
+__global__ __launch_bounds__(256) void log_approx_err_kernel(unsigned first, unsigned count,
+                                                             unsigned long long *__restrict__ out)
+{
+    double m = 0.0;
+    for (unsigned long long i = (unsigned long long)blockIdx.x * blockDim.x + threadIdx.x; i < count;
+         i += (unsigned long long)gridDim.x * blockDim.x) {
+        const float x = bits_f(first + (unsigned)i);
+        const double e = fabs((double)__builtin_amdgcn_logf(x) * 0.69314718055994530942 - (double)mdq_logf(x));
+        m = e > m ? e : m;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const double o = __shfl_xor(m, off, 64);
+        m = o > m ? o : m;
+    }
+    if ((threadIdx.x & 63) == 0) atomicMax(out, (unsigned long long)__double_as_longlong(m));
+}
+
+hipError_t launch_log_approx_err(unsigned first, unsigned count, unsigned long long *out, hipStream_t s)
+{
+    if (count == 0) return hipSuccess;
+    unsigned long long blocks = ((unsigned long long)count + 255) / 256;
+    int grid = (int)(blocks < 65536 ? blocks : 65536);
+    hipLaunchKernelGGL(log_approx_err_kernel, dim3(grid), dim3(256), 0, s, first, count, out);
+    return hipGetLastError();
+}
+
 hipError_t launch_math(int which, const float *x, float *y, long long n, hipStream_t s)
 {
     if (n <= 0) return hipSuccess;

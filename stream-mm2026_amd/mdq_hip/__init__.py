@@ -276,6 +276,16 @@ def grad_stats(grads: Sequence[torch.Tensor], out: Optional[torch.Tensor] = None
     return out
 
 
+def device_log_approx_error(first: int, count: int, device="cuda:0") -> float:
+    """max |v_log_f32(x) ln 2 - log x| over the floats with bit patterns first .. first+count-1,
+    computed on the device in fp64 (the bound behind the step kernel's fast v-code path)."""
+    dev = torch.device(device)
+    out = torch.zeros(1, dtype=torch.int64, device=dev)
+    with torch.cuda.device(dev):
+        check(lib().stq_device_log_approx_error(int(first), int(count), out.data_ptr(), _capi.stream_handle(dev)))
+    return float(out.cpu().view(torch.float64).item())
+
+
 def device_math(which: str, x: torch.Tensor) -> torch.Tensor:
     """Device e^x (``which='exp'``) or log x (``'log'``) with the kernels' own fp32 code."""
     assert x.is_cuda and x.dtype == torch.float32 and x.is_contiguous()

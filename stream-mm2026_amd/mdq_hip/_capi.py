@@ -39,6 +39,7 @@ EXPORTED_SYMBOLS = (
     "stq_abi_version",
     "stq_device_math",
     "stq_device_math_digests",
+    "stq_device_log_approx_error",
     "stq_host_math",
     "stq_host_round_half_away",
     "stq_host_div_code_range",
@@ -114,6 +115,8 @@ def lib() -> ctypes.CDLL:
     L.stq_device_math.restype = ctypes.c_int
     L.stq_device_math_digests.argtypes = [i32, u32, u32, u32, vp, vp]
     L.stq_device_math_digests.restype = ctypes.c_int
+    L.stq_device_log_approx_error.argtypes = [u32, u32, vp, vp]
+    L.stq_device_log_approx_error.restype = ctypes.c_int
     L.stq_host_math.argtypes = [i32, vp, vp, i64]
     L.stq_host_math.restype = None
     L.stq_host_round_half_away.argtypes = [vp, vp, vp, i64, i32]
