@@ -333,6 +333,45 @@ def bit_decision(steps: int):
     return out
 
 
+def transitions(reps: int):
+    """Wall time of optimizer steps that change the code storage (first step int16 -> 4-bit
+    nibbles, then 4 -> 8 -> 16 -> 4 bits), with the one-launch device conversions and with the
+    reference's per-tensor torch passes, on the GPT-2 small and LLaMA-7B tensor sets."""
+    import torch
+
+    from stquant_opt_fused_io import MDQAdamWSimpleFusedIO
+
+    dev = torch.device("cuda:0")
+    out = {}
+    for cfg in ("gpt2", "llama7b"):
+        shapes = CONFIGS[cfg][0]()
+        res = {}
+        for mode in ("device", "torch"):
+            times = {}
+            for rep in range(reps):
+                params = []
+                for _, n in shapes:
+                    p = torch.nn.Parameter(torch.empty(n, device=dev).normal_(0.0, 0.02))
+                    p.grad = torch.empty(n, device=dev).normal_(0.0, 1e-3)
+                    params.append(p)
+                opt = MDQAdamWSimpleFusedIO(params, bits=4, block_size=128, sync_timing=False)
+                opt._device_transitions = mode == "device"
+                for label, bits in (("first step 16->4", 4), ("4->8", 8), ("8->16", 16), ("16->4", 4),
+                                    ("steady 4", 4)):
+                    opt.param_groups[0]["bits"] = bits
+                    torch.cuda.synchronize()
+                    t0 = time.perf_counter()
+                    opt.step()
+                    torch.cuda.synchronize()
+                    times.setdefault(label, []).append((time.perf_counter() - t0) * 1e3)
+                del opt, params
+                torch.cuda.empty_cache()
+            res[mode] = {k: min(v) for k, v in times.items()}
+            log(f"transitions {cfg} {mode}: " + ", ".join(f"{k} {v:.1f} ms" for k, v in res[mode].items()))
+        out[cfg] = {"tensors": len(shapes), "params": sum(n for _, n in shapes), **res}
+    return out
+
+
 def cpu_baseline(gdt: str, bits: int, B: int, seconds: float):
     """The oracle (C, OpenMP over quant blocks) on a 2^24-param slice of the same
     workload, repeated for about `seconds`; params/s over this host's cores."""
@@ -378,6 +417,8 @@ def main():
                     help="BASELINE config 3: GPT-2 small pretraining, stochastic vs nearest vs AdamW")
     ap.add_argument("--e2e-steps", type=int, default=300)
     ap.add_argument("--e2e-out", default=None, help="also write the loss histories as JSON here")
+    ap.add_argument("--transitions", action="store_true",
+                    help="time storage-changing optimizer steps, device conversions vs torch passes")
     ap.add_argument("--bit-decision", action="store_true",
                     help="time the update-step bit decision, fused vs the reference's per-tensor path")
     ap.add_argument("--copy-gib", type=float, default=0.0,
@@ -396,6 +437,10 @@ def main():
         res = sweep_config5(dev, args.steps, args.warmup)
         print(json.dumps({"metric": "config 5 sweep: params/s and HBM GB/s per point", "n_gpus": 1,
                           "steps": args.steps, "warmup": args.warmup, "data": "synthetic", **res}), flush=True)
+        return
+    if args.transitions:
+        print(json.dumps({"metric": "optimizer step wall ms on bit-width transitions", "n_gpus": 1,
+                          "data": "synthetic", "configs": transitions(max(1, args.steps // 10))}), flush=True)
         return
     if args.bit_decision:
         print(json.dumps({"metric": "MDQ bit decision per update step (ms)", "n_gpus": 1, "steps": args.steps,

@@ -144,6 +144,37 @@ int stq_multi_tensor_mdq_adamw(const stq_tensor *tensors, int n_tensors,
 int stq_multi_tensor_grad_stats(const void *const *grads, const int64_t *numels, int n_tensors,
                                 int grad_dtype, float *stats, void *stream);
 
+/* Code storage classes of stq_code_convert (the m/v code layouts the step kernels read). */
+enum {
+    STQ_STORE_P4 = 0,   /* uint8 bytes (v << 4) | (m + 8), no separate v array */
+    STQ_STORE_S8 = 1,   /* int8 m, uint8 v   */
+    STQ_STORE_S16 = 2,  /* int16 m, uint16 v */
+    STQ_STORE_S32 = 3   /* int32 m, uint32 v */
+};
+
+typedef struct stq_code_convert {
+    const void *src_exp_avg;     /* m codes (or packed bytes) in src_storage */
+    const void *src_exp_avg_sq;  /* v codes in src_storage (unused for STQ_STORE_P4) */
+    void *dst_exp_avg;           /* m codes (or packed bytes) in dst_storage */
+    void *dst_exp_avg_sq;        /* v codes in dst_storage (unused for STQ_STORE_P4) */
+    int64_t numel;
+    int32_t src_storage, dst_storage;
+} stq_code_convert;
+
+/*
+ * Re-stores the m/v codes of n_tensors tensors from one storage class to
+ * another, in one launch: the value map decode(src) -> clamp to dst's range
+ * -> encode(dst), where P4 decodes to m = (b & 15) - 8, v = b >> 4 and encodes
+ * as clamp(m + 8, 0, 15) | clamp(v, 0, 15) << 4, and the integer classes clamp
+ * m to their signed and v to their unsigned range.  This is every storage
+ * change MDQAdamWSimple makes on a bit-width change: the alignment before the
+ * step and the nibble packing after it
+ * (/root/reference/CUDA/stquant_opt_simple.py:140-210), which the reference
+ * runs as several torch passes per tensor.  Source and destination must not
+ * overlap.
+ */
+int stq_multi_tensor_convert_codes(const stq_code_convert *items, int n_tensors, void *stream);
+
 /* Last error message of this thread ("" when none). */
 const char *stq_last_error(void);
 

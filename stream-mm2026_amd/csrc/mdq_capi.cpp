@@ -19,6 +19,7 @@
 #include "mdq_desc.h"
 #include "mdq_launch.h"
 #include "mdq_math.h"
+#include "mdq_convert.h"
 #include "mdq_stats.h"
 
 namespace {
@@ -376,6 +377,60 @@ int run(const stq_tensor *tensors, int n_tensors, int grad_dt, int ea_dt, int ea
                              reinterpret_cast<hipStream_t>(stream));
 }
 
+// stq_multi_tensor_convert_codes: descriptors and tile starts in one ring slot.
+int run_convert(const stq_code_convert *items, int n, hipStream_t stream)
+{
+    g_err.clear();
+    if (n < 0 || (n > 0 && !items)) return fail(STQ_ERR_INVALID, "convert_codes: bad tensor list");
+    std::vector<mdq::ConvDesc> d;
+    d.reserve((size_t)n);
+    int64_t tiles = 0;
+    for (int i = 0; i < n; ++i) {
+        const stq_code_convert &c = items[i];
+        if (c.numel < 0) return fail(STQ_ERR_INVALID, "tensor %d: negative numel", i);
+        if (c.src_storage < STQ_STORE_P4 || c.src_storage > STQ_STORE_S32 || c.dst_storage < STQ_STORE_P4 ||
+            c.dst_storage > STQ_STORE_S32)
+            return fail(STQ_ERR_INVALID, "tensor %d: storage must be STQ_STORE_P4 .. STQ_STORE_S32", i);
+        if (c.numel == 0) continue;
+        if (!c.src_exp_avg || !c.dst_exp_avg || (c.src_storage != STQ_STORE_P4 && !c.src_exp_avg_sq) ||
+            (c.dst_storage != STQ_STORE_P4 && !c.dst_exp_avg_sq))
+            return fail(STQ_ERR_INVALID, "tensor %d: null code pointer", i);
+        mdq::ConvDesc e{};
+        e.src_m = c.src_exp_avg;
+        e.src_v = c.src_exp_avg_sq;
+        e.dst_m = c.dst_exp_avg;
+        e.dst_v = c.dst_exp_avg_sq;
+        e.numel = c.numel;
+        e.tile_begin = tiles;
+        e.src = c.src_storage;
+        e.dst = c.dst_storage;
+        tiles += (c.numel + mdq::CONV_TILE - 1) / mdq::CONV_TILE;
+        d.push_back(e);
+    }
+    if (d.empty()) return STQ_OK;
+    if (tiles > 0x7fffffffLL)
+        return fail(STQ_ERR_INVALID, "too many tiles in one call (%lld); split the tensor list", (long long)tiles);
+    DevCtx *ctx = nullptr;
+    int rc = get_ctx(&ctx);
+    if (rc != STQ_OK) return rc;
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    const size_t m = d.size();
+    const size_t need = m * (sizeof(mdq::ConvDesc) + sizeof(long long));
+    Slot *s = nullptr;
+    rc = take_slot(ctx, need, &s);
+    if (rc != STQ_OK) return rc;
+    std::memcpy(s->host, d.data(), m * sizeof(mdq::ConvDesc));
+    long long *tb = reinterpret_cast<long long *>(s->host + m * sizeof(mdq::ConvDesc));
+    for (size_t i = 0; i < m; ++i) tb[i] = d[i].tile_begin;
+    hipError_t e = hipMemcpyAsync(s->dev, s->host, need, hipMemcpyHostToDevice, stream);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(descriptors)");
+    e = mdq::launch_convert(reinterpret_cast<const mdq::ConvDesc *>(s->dev),
+                            reinterpret_cast<const long long *>(s->dev + m * sizeof(mdq::ConvDesc)), (int)m,
+                            tiles, stream);
+    if (e != hipSuccess) return hip_fail(e, "convert launch");
+    return release_slot(s, stream);
+}
+
 }  // namespace
 
 extern "C" {
@@ -429,6 +484,11 @@ int stq_multi_tensor_grad_stats(const void *const *grads, const int64_t *numels,
                                 int grad_dtype, float *stats, void *stream)
 {
     return run_grad_stats(grads, numels, n_tensors, grad_dtype, stats, reinterpret_cast<hipStream_t>(stream));
+}
+
+int stq_multi_tensor_convert_codes(const stq_code_convert *items, int n_tensors, void *stream)
+{
+    return run_convert(items, n_tensors, reinterpret_cast<hipStream_t>(stream));
 }
 
 const char *stq_last_error(void) { return g_err.c_str(); }

@@ -276,6 +276,59 @@ def grad_stats(grads: Sequence[torch.Tensor], out: Optional[torch.Tensor] = None
     return out
 
 
+STORE_P4, STORE_S8, STORE_S16, STORE_S32 = 0, 1, 2, 3
+_STORE_DTYPES = {STORE_S8: (torch.int8, torch.uint8), STORE_S16: (torch.int16, torch.uint16),
+                 STORE_S32: (torch.int32, torch.uint32)}
+# stq_code_convert: 4 pointers, int64 numel, two int32 storages (48 bytes)
+STQ_CONVERT_DTYPE = np.dtype([("src_m", np.uint64), ("src_v", np.uint64), ("dst_m", np.uint64),
+                              ("dst_v", np.uint64), ("numel", np.int64), ("src", np.int32), ("dst", np.int32)])
+
+
+def storage_of(exp_avg: torch.Tensor, exp_avg_sq: torch.Tensor) -> int:
+    """The code storage class of a state's (exp_avg, exp_avg_sq) pair."""
+    if exp_avg.dtype == torch.uint8 and exp_avg_sq.numel() == 0:
+        return STORE_P4
+    for st, (dm, dv) in _STORE_DTYPES.items():
+        if exp_avg.dtype == dm and exp_avg_sq.dtype == dv and exp_avg_sq.numel() == exp_avg.numel():
+            return st
+    raise RuntimeError(f"no code storage class for exp_avg {exp_avg.dtype} / exp_avg_sq {exp_avg_sq.dtype}"
+                       f"[{exp_avg_sq.numel()}]")
+
+
+def empty_codes(like: torch.Tensor, storage: int):
+    """Uninitialised (exp_avg, exp_avg_sq) of ``like``'s shape and device in ``storage``."""
+    if storage == STORE_P4:
+        return (torch.empty_like(like, dtype=torch.uint8, memory_format=torch.contiguous_format),
+                torch.empty(0, dtype=torch.uint8, device=like.device))
+    dm, dv = _STORE_DTYPES[storage]
+    return (torch.empty_like(like, dtype=dm, memory_format=torch.contiguous_format),
+            torch.empty_like(like, dtype=dv, memory_format=torch.contiguous_format))
+
+
+def convert_codes(items) -> None:
+    """Re-store codes for a list of ``(src_exp_avg, src_exp_avg_sq, dst_exp_avg, dst_exp_avg_sq)``
+    in one launch (storage classes inferred from the dtypes): decode the source, clamp to the
+    destination's range, encode -- every storage change of stquant_opt_simple.py:140-210."""
+    items = list(items)
+    if not items:
+        return
+    arr = np.zeros(len(items), dtype=STQ_CONVERT_DTYPE)
+    dev = items[0][0].device
+    for k, (sm, sv, dm, dv) in enumerate(items):
+        for t in (sm, sv, dm, dv):
+            if t.numel() and (t.device != dev or not t.is_contiguous()):
+                raise RuntimeError("convert_codes: code tensors must be contiguous and on one CUDA device")
+        if dm.numel() != sm.numel():
+            raise RuntimeError("convert_codes: source and destination sizes differ")
+        arr[k] = (sm.data_ptr() if sm.numel() else 0, sv.data_ptr() if sv.numel() else 0,
+                  dm.data_ptr() if dm.numel() else 0, dv.data_ptr() if dv.numel() else 0, sm.numel(),
+                  storage_of(sm, sv), storage_of(dm, dv))
+    if dev.type != "cuda":
+        raise RuntimeError("convert_codes: code tensors must be CUDA tensors")
+    with torch.cuda.device(dev):
+        check(lib().stq_multi_tensor_convert_codes(arr.ctypes.data, len(items), _capi.stream_handle(dev)))
+
+
 def device_log_approx_error(first: int, count: int, device="cuda:0") -> float:
     """max |v_log_f32(x) ln 2 - log x| over the floats with bit patterns first .. first+count-1,
     computed on the device in fp64 (the bound behind the step kernel's fast v-code path)."""

@@ -35,6 +35,7 @@ EXPORTED_SYMBOLS = (
     "stq_fused_mdq_adamw",
     "stq_multi_tensor_mdq_adamw",
     "stq_multi_tensor_grad_stats",
+    "stq_multi_tensor_convert_codes",
     "stq_last_error",
     "stq_abi_version",
     "stq_device_math",
@@ -105,6 +106,8 @@ def lib() -> ctypes.CDLL:
     L.stq_multi_tensor_mdq_adamw.argtypes = [
         ctypes.POINTER(StqTensor), i32, i32, i32, i32, i32, i32, u64, vp, i64, vp]
     L.stq_multi_tensor_mdq_adamw.restype = ctypes.c_int
+    L.stq_multi_tensor_convert_codes.argtypes = [vp, i32, vp]
+    L.stq_multi_tensor_convert_codes.restype = ctypes.c_int
     L.stq_multi_tensor_grad_stats.argtypes = [vp, vp, i32, i32, vp, vp]
     L.stq_multi_tensor_grad_stats.restype = ctypes.c_int
     L.stq_last_error.argtypes = []

@@ -88,6 +88,9 @@ class MDQAdamWSimple(Optimizer):
     _KERNEL_PROF_SLOTS = 5
     # launch-plan class of ``_run_kernels`` (a test harness substitutes its own executor)
     _plan_cls = mdq_hip.MultiTensorPlan
+    # storage changes of CUDA tensors in one conversion launch per step; False keeps the
+    # reference's per-tensor torch passes (same results)
+    _device_transitions = True
 
     def add_param_group(self, param_group):
         self.__dict__["_steady"] = None
@@ -323,12 +326,74 @@ class MDQAdamWSimple(Optimizer):
         state["step"] += 1
         if self._storage_matches_bits(state, bits):
             return False
-        self._align_momentum_storage(state, bits)
+        pending = self.__dict__.get("_pending_align")
+        if pending is not None and state["exp_avg"].is_cuda:
+            pending.append((state, bits))              # one conversion launch for all (_flush_align)
+        else:
+            self._align_momentum_storage(state, bits)
         return True
 
     def _finish_update(self, p):
         state = self.state[p]
-        self._pack_momentum_storage(state, int(state["current_bit"]))
+        bits = int(state["current_bit"])
+        pending = self.__dict__.get("_pending_pack")
+        if pending is not None and state["exp_avg"].is_cuda:
+            pending.append((state, bits))
+        else:
+            self._pack_momentum_storage(state, bits)
+
+    @staticmethod
+    def _aligned_storage(bits: int) -> int:
+        """The code storage _align_momentum_storage leaves for ``bits`` (:166-198)."""
+        if bits >= 32:
+            return mdq_hip.STORE_S32
+        if bits > 8:
+            return mdq_hip.STORE_S16
+        return mdq_hip.STORE_S8
+
+    @staticmethod
+    def _convert_states(moves):
+        """Re-store the codes of ``[(state, dst_storage)]`` with one conversion launch."""
+        items, news = [], []
+        for state, dst in moves:
+            ea, easq = state["exp_avg"], state["exp_avg_sq"]
+            nm, nv = mdq_hip.empty_codes(ea, dst)
+            items.append((ea, easq, nm, nv))
+            news.append((state, nm, nv))
+        mdq_hip.convert_codes(items)
+        for state, nm, nv in news:
+            state["exp_avg"], state["exp_avg_sq"] = nm, nv
+
+    def _flush_align(self):
+        """Device version of _align_momentum_storage for all deferred tensors: the same value map
+        (unpack nibbles, widen, or clamp to the narrower range; :140-198) in one launch."""
+        pending, self._pending_align = self.__dict__.get("_pending_align") or [], None
+        moves = []
+        for state, bits in pending:
+            if state["exp_avg"].numel() == 0:          # the reference's dtype rules for empty tensors
+                self._align_momentum_storage(state, bits)
+                continue
+            src = mdq_hip.storage_of(state["exp_avg"], state["exp_avg_sq"])
+            dst = self._aligned_storage(bits)
+            if src != dst:
+                moves.append((state, dst))
+        if moves:
+            self._convert_states(moves)
+
+    def _flush_pack(self):
+        """Device version of _pack_momentum_storage after the step: 4-bit tensors in int8/uint8
+        storage go to nibbles (:214-219) in one launch; after alignment every other width
+        is already in its final storage."""
+        pending, self._pending_pack = self.__dict__.get("_pending_pack") or [], None
+        moves = []
+        for state, bits in pending:
+            if (bits == 4 and state["exp_avg"].numel() > 0
+                    and mdq_hip.storage_of(state["exp_avg"], state["exp_avg_sq"]) == mdq_hip.STORE_S8):
+                moves.append((state, mdq_hip.STORE_P4))
+            else:
+                self._pack_momentum_storage(state, bits)
+        if moves:
+            self._convert_states(moves)
 
     def _launch_fused_update(self, p, group):
         """Single-tensor update with the reference's per-tensor timing (:231-280)."""
@@ -686,7 +751,11 @@ class MDQAdamWSimple(Optimizer):
         re-pack; timing keys as the per-tensor loop of :501-502 fills them."""
         dev = params_with_grad[0][0].device
         t0 = time.perf_counter()
-        repack = [self._prepare_update(p, g) for p, g in params_with_grad]
+        self._pending_align = [] if self._device_transitions else None
+        try:
+            repack = [self._prepare_update(p, g) for p, g in params_with_grad]
+        finally:
+            self._flush_align()
         unpack_ms = (time.perf_counter() - t0) * 1000.0
         if self.sync_timing:
             self._sync_device(dev)
@@ -696,9 +765,13 @@ class MDQAdamWSimple(Optimizer):
             self._sync_device(dev)
         kernel_ms = (time.perf_counter() - tk0) * 1000.0
         t1 = time.perf_counter()
-        for (p, _g), rp in zip(params_with_grad, repack):
-            if rp:
-                self._finish_update(p)
+        self._pending_pack = [] if self._device_transitions else None
+        try:
+            for (p, _g), rp in zip(params_with_grad, repack):
+                if rp:
+                    self._finish_update(p)
+        finally:
+            self._flush_pack()
         pack_ms = (time.perf_counter() - t1) * 1000.0
         lt = self.last_step_timings
         lt["quant_dequant_unpack_ms"] += unpack_ms
