@@ -151,8 +151,8 @@ int make_desc(const stq_tensor &t, int storage, int grad_dt, int B, MdqDesc &d)
     d.tensor_id = t.tensor_id;
     const int gb = grad_dt == STQ_FLOAT ? 4 : 2;
     const int cb = code_bytes(storage);
-    // full tiles move codes in 4-element quads (4 * cb bytes), int8/uint8 codes in 8-byte pairs
-    const int ca = storage == mdq::ST_S8 ? 8 : 4 * cb;
+    // full tiles move codes in 4-element quads (4 * cb bytes), 1-byte codes in 8-byte pairs
+    const int ca = (storage == mdq::ST_S8 || storage == mdq::ST_P4) ? 8 : 4 * cb;
     bool al = is_aligned(t.p, 16) && is_aligned(t.grad, 4 * gb) && is_aligned(t.exp_avg, ca) &&
               (storage == mdq::ST_P4 || is_aligned(t.exp_avg_sq, ca));
     d.flags = al ? mdq::DF_ALIGNED : 0u;

@@ -72,13 +72,12 @@ __device__ __forceinline__ void st_g(T v, void *a) { *(MDQ_GLOBAL T *)a = v; }
 template <int ST, int LOG2B>
 constexpr bool paired_codes()
 {
-    // int8 + uint8 codes, 16 or 32 lanes per block: each lane moves its codes as one
-    // contiguous 8-byte access per array (full 128-byte lines per instruction) and swaps
-    // half of them with lane j ^ LPB/2, so the lane's quads are k*LPB + pi(j) with
-    // pi(j) = 2 (j mod LPB/2) + j div LPB/2 for every array.  Measured on the LLaMA
-    // set's access pattern: -2.7 % time against 4-byte quad accesses.  (Packed 4-bit
-    // codes gain nothing: the permuted p / g lane order costs what the codes save.)
-    return ST == ST_S8 && (Cfg<LOG2B>::LPB == 16 || Cfg<LOG2B>::LPB == 32);
+    // 1-byte codes (packed 4-bit, or int8 + uint8), 16 or 32 lanes per block: each lane
+    // moves its codes as one contiguous 8-byte access per array (full 128-byte lines per
+    // instruction) and swaps half of them with lane j ^ LPB/2, so the lane's quads are
+    // k*LPB + pi(j) with pi(j) = 2 (j mod LPB/2) + j div LPB/2 for every array.  LLaMA set,
+    // same-box A/B against 4-byte quad accesses: packed 4-bit -3.4 %, int8 + uint8 -6 %.
+    return (ST == ST_P4 || ST == ST_S8) && (Cfg<LOG2B>::LPB == 16 || Cfg<LOG2B>::LPB == 32);
 }
 
 // Quad k (0 .. QPL-1) of lane j within its quant block.
@@ -106,6 +105,25 @@ __device__ __forceinline__ uint32_t swap_half(uint32_t x)
     static_assert(H == 8 || H == 16, "lane pairs at distance 8 or 16");
     if constexpr (H == 8) return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x128, 0xF, 0xF, true);
     else return (uint32_t)__builtin_amdgcn_ds_swizzle((int)x, 0x401F);
+}
+
+// Paired code layout (paired_codes): lane j reads bytes [8j, 8j + 8) of its block's codes
+// (quads 2j, 2j + 1) and keeps / receives its own quads pi(j) (k = 0) and LPB + pi(j) (k = 1);
+// pair_out is the inverse for the store.
+template <int H>
+__device__ __forceinline__ uint32_t pair_in(vu2 w, int j, int k)
+{
+    const bool lo = j < H;
+    const uint32_t y = swap_half<H>(lo ? w.y : w.x);
+    return k == 0 ? (lo ? w.x : y) : (lo ? y : w.y);
+}
+
+template <int H>
+__device__ __forceinline__ vu2 pair_out(uint32_t q0, uint32_t q1, int j)
+{
+    const bool lo = j < H;
+    const uint32_t y = swap_half<H>(lo ? q1 : q0);
+    return lo ? vu2{q0, y} : vu2{y, q1};
 }
 
 // ---------------------------------------------------------------- grad loads
@@ -162,6 +180,32 @@ template <> struct CodeIO<ST_P4> {
         mc = (float)(b & 15u);
         vc = b >> 4;
     }
+    template <int H>
+    static __device__ __forceinline__ void load8(const MdqDesc &d, uint32_t blk_off, int j, float *mc, uint32_t *vc) {
+        const vu2 w = ld_nt<vu2>(static_cast<const uint8_t *>(d.code_m) + blk_off + 8 * j);
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t q = pair_in<H>(w, j, h);
+            const uint32_t lo = q & 0x0f0f0f0fu;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                mc[4 * h + k] = (float)((lo >> (8 * k)) & 0xffu);
+                vc[4 * h + k] = (q >> (8 * k + 4)) & 15u;
+            }
+        }
+    }
+    template <int H>
+    static __device__ __forceinline__ void store8f(const MdqDesc &d, uint32_t blk_off, int j, const float *pk) {
+        uint32_t q[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            uint32_t w = __builtin_amdgcn_cvt_pk_u8_f32(pk[4 * h + 0], 0, 0u);
+            w = __builtin_amdgcn_cvt_pk_u8_f32(pk[4 * h + 1], 1, w);
+            w = __builtin_amdgcn_cvt_pk_u8_f32(pk[4 * h + 2], 2, w);
+            q[h] = __builtin_amdgcn_cvt_pk_u8_f32(pk[4 * h + 3], 3, w);
+        }
+        st_nt<vu2>(pair_out<H>(q[0], q[1], j), static_cast<uint8_t *>(d.code_m) + blk_off + 8 * j);
+    }
     // byte values already formed as floats (exact integers 0..255)
     static __device__ __forceinline__ void store4f(const MdqDesc &d, int64_t i, const float *pk) {
         uint32_t w = __builtin_amdgcn_cvt_pk_u8_f32(pk[0], 0, 0u);
@@ -198,20 +242,6 @@ template <> struct CodeIO<ST_S8> {
     static __device__ __forceinline__ void load1(const MdqDesc &d, int64_t i, float &mc, uint32_t &vc) {
         mc = (float)ld_g<int8_t>(static_cast<const int8_t *>(d.code_m) + i);
         vc = ld_g<uint8_t>(static_cast<const uint8_t *>(d.code_v) + i);
-    }
-    // Paired layout (paired_codes): lane j reads bytes [8j, 8j + 8) of its block (quads 2j,
-    // 2j + 1) from both arrays and keeps / receives its quads pi(j) and LPB + pi(j).
-    template <int H>
-    static __device__ __forceinline__ uint32_t pair_in(vu2 w, int j, int k) {
-        const bool lo = j < H;
-        const uint32_t y = swap_half<H>(lo ? w.y : w.x);
-        return k == 0 ? (lo ? w.x : y) : (lo ? y : w.y);
-    }
-    template <int H>
-    static __device__ __forceinline__ vu2 pair_out(uint32_t q0, uint32_t q1, int j) {
-        const bool lo = j < H;
-        const uint32_t y = swap_half<H>(lo ? q1 : q0);
-        return lo ? vu2{q0, y} : vu2{y, q1};
     }
     template <int H>
     static __device__ __forceinline__ void load8(const MdqDesc &d, uint32_t blk_off, int j, float *mc, uint32_t *vc) {
@@ -722,12 +752,17 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
 #pragma unroll
         for (int k = 0; k < C::QPL; ++k) {
             const uint32_t i = lbase + 4 * lane_quad<ST, LOG2B>(j, k);
-            if constexpr (ST == ST_P4) CodeIO<ST>::store4f(dt, i, pk + 4 * k);
-            else if constexpr (!paired_codes<ST, LOG2B>()) CodeIO<ST>::store4(dt, i, qmi + 4 * k, qvi + 4 * k);
+            if constexpr (!paired_codes<ST, LOG2B>()) {
+                if constexpr (ST == ST_P4) CodeIO<ST>::store4f(dt, i, pk + 4 * k);
+                else CodeIO<ST>::store4(dt, i, qmi + 4 * k, qvi + 4 * k);
+            }
             vf4 o = {pv[4 * k + 0], pv[4 * k + 1], pv[4 * k + 2], pv[4 * k + 3]};
             st_nt<vf4>(o, dt.p + i);
         }
-        if constexpr (paired_codes<ST, LOG2B>()) CodeIO<ST>::template store8<LPB / 2>(dt, lbase, j, qmi, qvi);
+        if constexpr (paired_codes<ST, LOG2B>()) {
+            if constexpr (ST == ST_P4) CodeIO<ST>::template store8f<LPB / 2>(dt, lbase, j, pk);
+            else CodeIO<ST>::template store8<LPB / 2>(dt, lbase, j, qmi, qvi);
+        }
     } else {
 #pragma unroll
         for (int e = 0; e < EPL; ++e) {
