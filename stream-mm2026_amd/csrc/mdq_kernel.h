@@ -72,12 +72,12 @@ __device__ __forceinline__ void st_g(T v, void *a) { *(MDQ_GLOBAL T *)a = v; }
 template <int ST, int LOG2B>
 constexpr bool paired_codes()
 {
-    // 1-byte codes (packed 4-bit, or int8 + uint8), 16 or 32 lanes per block: each lane
+    // 1-byte codes (packed 4-bit, or int8 + uint8), 8, 16 or 32 lanes per block: each lane
     // moves its codes as one contiguous 8-byte access per array (full 128-byte lines per
     // instruction) and swaps half of them with lane j ^ LPB/2, so the lane's quads are
     // k*LPB + pi(j) with pi(j) = 2 (j mod LPB/2) + j div LPB/2 for every array.  LLaMA set,
     // same-box A/B against 4-byte quad accesses: packed 4-bit -3.4 %, int8 + uint8 -6 %.
-    return (ST == ST_P4 || ST == ST_S8) && (Cfg<LOG2B>::LPB == 16 || Cfg<LOG2B>::LPB == 32);
+    return (ST == ST_P4 || ST == ST_S8) && (Cfg<LOG2B>::LPB == 8 || Cfg<LOG2B>::LPB == 16 || Cfg<LOG2B>::LPB == 32);
 }
 
 // Quad k (0 .. QPL-1) of lane j within its quant block.
@@ -98,13 +98,14 @@ __device__ __forceinline__ int elem_off(int j, int e)
     else return e;
 }
 
-// x from lane j ^ H (H = 8: DPP row_ror:8 within a 16-lane row; H = 16: ds_swizzle xor 16).
+// x from lane j ^ H (H = 8: DPP row_ror:8 within a 16-lane row; H = 4 or 16: ds_swizzle in
+// bit mode with xor mask H).
 template <int H>
 __device__ __forceinline__ uint32_t swap_half(uint32_t x)
 {
-    static_assert(H == 8 || H == 16, "lane pairs at distance 8 or 16");
+    static_assert(H == 4 || H == 8 || H == 16, "lane pairs at distance 4, 8 or 16");
     if constexpr (H == 8) return (uint32_t)__builtin_amdgcn_mov_dpp((int)x, 0x128, 0xF, 0xF, true);
-    else return (uint32_t)__builtin_amdgcn_ds_swizzle((int)x, 0x401F);
+    else return (uint32_t)__builtin_amdgcn_ds_swizzle((int)x, (H << 10) | 0x1F);
 }
 
 // Paired code layout (paired_codes): lane j reads bytes [8j, 8j + 8) of its block's codes
