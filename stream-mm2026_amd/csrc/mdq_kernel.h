@@ -523,14 +523,14 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
     }
     if (prof_on) { unsigned long long t = clock64(); pa.c[1] += t - t0; t0 = t; }
 
-    // Fast v-code path: nearest rounding, code width <= 8 bits, a one-wave
-    // tile with every element inside the tensor and every x = v + 1e-12 a
-    // finite float >= 1e-12 (wave-uniform).  log is non-decreasing on that
+    // Fast v-code path: code width <= 8 bits, a one-wave tile with every
+    // element inside the tensor and every x = v + 1e-12 a finite float >= 1e-12
+    // (wave-uniform).  log is non-decreasing on that
     // range (checked for every float), so the block's max / min of log x are
     // the logs of its max / min x: two exact logs per lane instead of one per
     // element.  The per-element v codes then come from the hardware log (see
     // the requant below).
-    constexpr bool FAST_OK = FULL && !SR && C::WAVES == 1;
+    constexpr bool FAST_OK = FULL && C::WAVES == 1;
     bool fastv = false;
     if constexpr (FAST_OK) {
         if (d.bits <= 8u) {
@@ -659,10 +659,42 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
                     uv[e] = mdq_u16_uniform(ww >> 16);
                 }
             }
+            if (fastv) {
+                // The exact code is floor(T), T = fl(fma(u, fl(1/dv), uv)), u = fl(log x - vmin).
+                // Z = fl(z + uv) with z = fl(log2_hw(x) * c1 + c0) as in the nearest path
+                // differs from T by at most E + 4 (QV + 2) 2^-24 (E: the nearest path's bound;
+                // the rest: the roundings of u / dv vs u * fl(1/dv), of T and of Z).  Where Z is
+                // farther than that from an integer, floor(Z) is the code; the other elements
+                // take the exact path.
+                const float r = __builtin_amdgcn_rcpf(dv);
+                const float c1 = 0.69314718f * r;
+                const float c0 = -s_vmin * r;
+                const float L = fmaxf(fabsf(lmax), fabsf(lmin));
+                const float ep = (fma_(L, 1.3e-6f, MDQ_LOG_APPROX_ERR) * r + fma_(d.qvf + 2.0f, 2.4e-7f, 0.0f)) *
+                                 1.001f;
+                bool redo[EPL];
+                bool any = false;
 #pragma unroll
-            for (int e = 0; e < EPL; ++e) {
-                qmf[e] = floor_(fma_(m[e], inv_dm, um[e]));
-                qvf[e] = floor_(fma_(lv[e] - s_vmin, inv_dv, uv[e]));
+                for (int e = 0; e < EPL; ++e) {
+                    qmf[e] = floor_(fma_(m[e], inv_dm, um[e]));
+                    const float Z = fma_(__builtin_amdgcn_logf(v[e] + 1e-12f), c1, c0) + uv[e];
+                    const float fz = floor_(Z);
+                    const float f = Z - fz;
+                    qvf[e] = fz;
+                    redo[e] = f <= ep || f >= 1.0f - ep;
+                    any = any || redo[e];
+                }
+                if (__builtin_amdgcn_ballot_w64(any)) {
+#pragma unroll
+                    for (int e = 0; e < EPL; ++e)
+                        if (redo[e]) qvf[e] = floor_(fma_(mdq_logf(v[e] + 1e-12f) - s_vmin, inv_dv, uv[e]));
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) {
+                    qmf[e] = floor_(fma_(m[e], inv_dm, um[e]));
+                    qvf[e] = floor_(fma_(lv[e] - s_vmin, inv_dv, uv[e]));
+                }
             }
         } else {
             const float hdm = 0.5f * dm, hdv = 0.5f * dv;
