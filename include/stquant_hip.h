@@ -112,7 +112,8 @@ typedef struct stq_tensor {
  * packed metadata buffer.  Per-element results are identical to calling
  * stq_fused_mdq_adamw once per tensor.  All tensors share the storage dtype
  * pair, the grad dtype, the block size and the rounding mode; step, bits and
- * the AdamW hyper-parameters are per tensor.
+ * the AdamW hyper-parameters are per tensor.  The tensors' arrays must not overlap one another
+ * (the tensors are stepped concurrently, not one after the other).
  *
  * No reference counterpart as one call: it replaces the per-tensor launch loop
  * of MDQAdamWSimple.step (/root/reference/CUDA/stquant_opt_simple.py:501-502
