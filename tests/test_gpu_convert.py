@@ -95,3 +95,56 @@ def test_rejects_bad_arguments():
                                 torch.zeros(9, dtype=torch.uint8, device=DEV))])       # size mismatch
     with pytest.raises(RuntimeError):
         mdq_hip.convert_codes([(a, torch.zeros(8, dtype=torch.int32, device=DEV), a, a)])  # no storage class
+
+
+_RANGE = {"p4": ((-8, 7), (0, 15)), "s8": ((-128, 127), (0, 255)), "s16": ((-32768, 32767), (0, 65535)),
+          "s32": ((-2 ** 31, 2 ** 31 - 1), (0, 2 ** 32 - 1))}
+_STORE = {"p4": mdq_hip.STORE_P4, "s8": mdq_hip.STORE_S8, "s16": mdq_hip.STORE_S16, "s32": mdq_hip.STORE_S32}
+
+
+def _decode(kind, cm, cv):
+    """(m, v) as int64 numpy arrays: P4 bytes give m = (b & 15) - 8, v = b >> 4."""
+    if kind == "p4":
+        b = cm.numpy().astype(np.int64)
+        return (b & 15) - 8, b >> 4
+    return as_i64(cm).numpy(), as_i64(cv).numpy()
+
+
+@pytest.mark.parametrize("src", list(SRC))
+@pytest.mark.parametrize("dst", list(SRC))
+def test_every_storage_pair_matches_the_value_map(src, dst):
+    """All 16 (src, dst) pairs the C ABI accepts, in one launch per pair: two whole-tile tensors
+    (vector path), a ragged one, and an unaligned view (storage offset 1: element path).  Every
+    code is decode(src) clamped to dst's range; P4 stores clamp(m + 8, 0, 15) | clamp(v, 0, 15) << 4."""
+    print(f"case: convert pair {src} -> {dst}", flush=True)
+    sizes = [4096 * 3, 8192, 4096 * 2 + 777, 5000]
+    items, want, outs = [], [], []
+    for k, n in enumerate(sizes):
+        unaligned = k == len(sizes) - 1
+        cm, cv = rand_codes(src, n + (1 if unaligned else 0), 1000 + 31 * k + 7 * len(src) + len(dst))
+        gm, gv = cm.to(DEV), cv.to(DEV)
+        if unaligned:
+            cm, gm = cm[1:], gm[1:]
+            if src != "p4":
+                cv, gv = cv[1:], gv[1:]
+        m, v = _decode(src, cm, cv)
+        (mlo, mhi), (vlo, vhi) = _RANGE[dst]
+        m, v = np.clip(m, mlo, mhi), np.clip(v, vlo, vhi)
+        want.append((m + 8) | (v << 4) if dst == "p4" else (m, v))
+        nm, nv = mdq_hip.empty_codes(gm, _STORE[dst])
+        if unaligned and dst != "p4":
+            # destination views at an odd element offset too
+            bm, bv = mdq_hip.empty_codes(torch.empty(n + 1, device=DEV), _STORE[dst])
+            nm, nv = bm[1:], bv[1:]
+        elif unaligned:
+            nm = torch.empty(n + 1, dtype=torch.uint8, device=DEV)[1:]
+        items.append((gm, gv, nm, nv))
+        outs.append((nm, nv))
+    mdq_hip.convert_codes(items)
+    torch.cuda.synchronize()
+    for (nm, nv), w, n in zip(outs, want, sizes):
+        if dst == "p4":
+            assert np.array_equal(nm.cpu().numpy().astype(np.int64), w), f"n={n}"
+        else:
+            assert np.array_equal(as_i64(nm.cpu()).numpy(), w[0]), f"m codes, n={n}"
+            assert np.array_equal(as_i64(nv.cpu()).numpy(), w[1]), f"v codes, n={n}"
