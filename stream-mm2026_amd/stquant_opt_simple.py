@@ -588,7 +588,11 @@ class MDQAdamWSimple(Optimizer):
         torch's ``Optimizer.load_state_dict`` casts every floating-point-param
         state tensor to the param dtype, turning integer codes into float32.
         The code values are small integers (exact in float32); each code tensor
-        is cast back to the integer dtype it had in ``state_dict``."""
+        is cast back to the integer dtype it had in ``state_dict``.  torch also
+        moves per-param state to the param's device, but not the global EMA
+        statistics; they are moved to the device of the first param (where the
+        bit decision computes them), so a checkpoint written on one device
+        resumes on another."""
         self._steady = None
         self.__dict__.pop("_plan_cache", None)
         saved_dtypes = {}
@@ -612,6 +616,11 @@ class MDQAdamWSimple(Optimizer):
             for k, dt in saved_dtypes.get(pid, {}).items():
                 if st[k].dtype != dt:
                     st[k] = st[k].to(dt)
+        if params:
+            for k in ("n_ema", "r_ema", "v_global_ema"):
+                v = getattr(self, k)
+                if torch.is_tensor(v) and v.device != params[0].device:
+                    setattr(self, k, v.to(params[0].device))
 
     # ------------------------------------------------------------------
     # step (stquant_opt_simple.py:383-508)
