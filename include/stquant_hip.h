@@ -176,6 +176,37 @@ typedef struct stq_code_convert {
  */
 int stq_multi_tensor_convert_codes(const stq_code_convert *items, int n_tensors, void *stream);
 
+/* Destination codes of one tensor of stq_multi_tensor_mdq_adamw_restore. */
+typedef struct stq_code_out {
+    void *exp_avg;              /* new m codes (or packed bytes) in dst_storage */
+    void *exp_avg_sq;           /* new v codes in dst_storage (unused for STQ_STORE_P4) */
+    int64_t exp_avg_numel;
+    int64_t exp_avg_sq_numel;
+} stq_code_out;
+
+/*
+ * A step that changes the code storage of every tensor in the list, in one
+ * launch: the multi-tensor step of stq_multi_tensor_mdq_adamw reading each
+ * tensor's codes from tensors[i].exp_avg / exp_avg_sq in src_storage and
+ * writing its new codes to out[i] in dst_storage (scales, params in place).
+ * The result is exactly that of MDQAdamWSimple's route for a tensor whose bit
+ * width changed (/root/reference/CUDA/stquant_opt_simple.py:231-280): align the
+ * old codes to the new width (:140-173: unpack nibbles, widen, or clamp to the
+ * int8 / int16 range, old scales kept), run the kernel at the new width, pack
+ * 4-bit codes into nibbles (:175-210) -- without the separate passes.
+ *
+ * Every tensor's bits must fit dst_storage as the reference stores that width:
+ * STQ_STORE_P4 for bits == 4, STQ_STORE_S8 for 1..8, STQ_STORE_S16 for 9..16,
+ * STQ_STORE_S32 for 32; src_storage != dst_storage; min(block_size, 1024) must
+ * be 64, 128 or 256.  Source and destination codes must not overlap.  Other
+ * arguments as stq_multi_tensor_mdq_adamw.
+ */
+int stq_multi_tensor_mdq_adamw_restore(const stq_tensor *tensors, const stq_code_out *out, int n_tensors,
+                                       int grad_dtype, int src_storage, int dst_storage,
+                                       int block_size, int rounding, uint64_t seed,
+                                       int64_t *profile_cycles, int64_t profile_numel,
+                                       void *stream);
+
 /* Last error message of this thread ("" when none). */
 const char *stq_last_error(void);
 

@@ -240,9 +240,10 @@ int release_slot(Slot *s, hipStream_t stream)
 
 // Uploads descs to a device slot on `stream` and launches.  The slot's pinned
 // staging buffer is reused only after the event recorded behind its previous
-// launch has completed.
-int upload_and_launch(const std::vector<MdqDesc> &descs, int storage, int grad_dt, int log2b, bool sr,
-                      int64_t total_tiles, unsigned long long *prof, uint64_t seed, hipStream_t stream)
+// launch has completed.  `storage` is the code storage the kernel writes; it
+// reads `src_storage` (the same, except on a storage-changing step).
+int upload_and_launch(const std::vector<MdqDesc> &descs, int src_storage, int storage, int grad_dt, int log2b,
+                      bool sr, int64_t total_tiles, unsigned long long *prof, uint64_t seed, hipStream_t stream)
 {
     DevCtx *ctx = nullptr;
     int rc = get_ctx(&ctx);
@@ -263,11 +264,21 @@ int upload_and_launch(const std::vector<MdqDesc> &descs, int storage, int grad_d
     const MdqDesc *dd = reinterpret_cast<const MdqDesc *>(s.dev);
     const int nd = (int)n;
     const int grid = 0;   // one workgroup per tile (total_tiles)
-    switch (storage) {
-    case mdq::ST_P4: e = mdq::launch_p4(dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream); break;
-    case mdq::ST_S8: e = mdq::launch_s8(dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream); break;
-    case mdq::ST_S16: e = mdq::launch_s16(dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream); break;
-    default: e = mdq::launch_s32(dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream); break;
+    const int src = src_storage;
+    if (src == storage) {
+        switch (storage) {
+        case mdq::ST_P4: e = mdq::launch_p4(dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream); break;
+        case mdq::ST_S8: e = mdq::launch_s8(dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream); break;
+        case mdq::ST_S16: e = mdq::launch_s16(dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream); break;
+        default: e = mdq::launch_s32(dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream); break;
+        }
+    } else {
+        switch (storage) {
+        case mdq::ST_P4: e = mdq::launch_tr_p4(src, dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream); break;
+        case mdq::ST_S8: e = mdq::launch_tr_s8(src, dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream); break;
+        case mdq::ST_S16: e = mdq::launch_tr_s16(src, dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream); break;
+        default: e = mdq::launch_tr_s32(src, dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream); break;
+        }
     }
     if (e != hipSuccess) return hip_fail(e, "kernel launch");
     return release_slot(&s, stream);
@@ -374,7 +385,98 @@ int run(const stq_tensor *tensors, int n_tensors, int grad_dt, int ea_dt, int ea
     if (descs.empty()) return STQ_OK;
     if (tiles > 0x7fffffffLL)
         return fail(STQ_ERR_INVALID, "too many tiles in one call (%lld); split the tensor list", (long long)tiles);
-    return upload_and_launch(descs, storage, grad_dt, log2b, rounding == STQ_ROUND_STOCHASTIC, tiles,
+    return upload_and_launch(descs, storage, storage, grad_dt, log2b, rounding == STQ_ROUND_STOCHASTIC, tiles,
+                             reinterpret_cast<unsigned long long *>(prof), seed,
+                             reinterpret_cast<hipStream_t>(stream));
+}
+
+// The storage MDQAdamWSimple leaves a `bits`-wide tensor in after a step
+// (stquant_opt_simple.py:140-210): nibbles at 4 bits, else int8 / int16 /
+// int32 by width; -1 for widths it cannot store (17..31).
+int final_storage(int bits)
+{
+    if (bits == 4) return mdq::ST_P4;
+    if (bits >= 1 && bits <= 8) return mdq::ST_S8;
+    if (bits >= 9 && bits <= 16) return mdq::ST_S16;
+    if (bits == 32) return mdq::ST_S32;
+    return -1;
+}
+
+bool ranges_overlap(const void *a, int64_t na, const void *b, int64_t nb)
+{
+    const uintptr_t a0 = (uintptr_t)a, b0 = (uintptr_t)b;
+    return na > 0 && nb > 0 && a0 < b0 + (uintptr_t)nb && b0 < a0 + (uintptr_t)na;
+}
+
+// stq_multi_tensor_mdq_adamw_restore: the step of `run` with source codes in
+// src_storage and destination codes in dst_storage.
+int run_restore(const stq_tensor *tensors, const stq_code_out *out, int n_tensors, int grad_dt, int src, int dst,
+                int block_size, int rounding, uint64_t seed, int64_t *prof, int64_t prof_numel, void *stream)
+{
+    g_err.clear();
+    if (prof_numel == 0) prof = nullptr;
+    int log2b = 0;
+    int rc = common_checks(grad_dt, block_size, rounding, prof, prof_numel, &log2b);
+    if (rc != STQ_OK) return rc;
+    if (n_tensors < 0 || (n_tensors > 0 && (!tensors || !out))) return fail(STQ_ERR_INVALID, "bad tensor list");
+    if (src < STQ_STORE_P4 || src > STQ_STORE_S32 || dst < STQ_STORE_P4 || dst > STQ_STORE_S32)
+        return fail(STQ_ERR_INVALID, "storage must be STQ_STORE_P4 .. STQ_STORE_S32");
+    if (src == dst) return fail(STQ_ERR_INVALID, "restore: source and destination storage are the same");
+    if (log2b < mdq::TRANSITION_LOG2B_MIN || log2b > mdq::TRANSITION_LOG2B_MAX)
+        return fail(STQ_ERR_INVALID, "restore: block size must be 64, 128 or 256, got %d", 1 << log2b);
+    const int B = 1 << log2b;
+    const int64_t te = mdq::tile_elems(B);
+    const int scb = code_bytes(src), dcb = code_bytes(dst);
+    const int sca = (src == mdq::ST_S8 || src == mdq::ST_P4) ? 8 : 4 * scb;
+    std::vector<MdqDesc> descs;
+    descs.reserve((size_t)n_tensors);
+    int64_t tiles = 0;
+    for (int i = 0; i < n_tensors; ++i) {
+        const stq_tensor &t = tensors[i];
+        const stq_code_out &o = out[i];
+        const std::string at = "tensor " + std::to_string(i) + ": ";
+        if (final_storage(t.bits) != dst && !(dst == mdq::ST_S8 && t.bits == 4))
+            return fail(STQ_ERR_INVALID, "%sbits=%d is not stored in destination storage %d", at.c_str(), t.bits, dst);
+        if (t.numel < 0) return fail(STQ_ERR_INVALID, "%snumel must be >= 0", at.c_str());
+        if (src == mdq::ST_P4 ? t.exp_avg_numel != t.numel
+                              : (t.exp_avg_numel < t.numel || t.exp_avg_sq_numel < t.numel))
+            return fail(STQ_ERR_INVALID, "%ssource codes must hold numel (%lld) codes", at.c_str(), (long long)t.numel);
+        if (t.numel > 0 && (!t.exp_avg || (src != mdq::ST_P4 && !t.exp_avg_sq)))
+            return fail(STQ_ERR_INVALID, "%snull source code pointer", at.c_str());
+        // the destination arrays are checked as the step's own codes
+        stq_tensor td = t;
+        td.exp_avg = o.exp_avg;
+        td.exp_avg_sq = o.exp_avg_sq;
+        td.exp_avg_numel = o.exp_avg_numel;
+        td.exp_avg_sq_numel = dst == mdq::ST_P4 ? 0 : o.exp_avg_sq_numel;
+        MdqDesc d;
+        rc = make_desc(td, dst, grad_dt, B, d);
+        if (rc != STQ_OK) {
+            g_err = at + g_err;
+            return rc;
+        }
+        if (t.numel == 0) continue;
+        const int64_t sb = t.numel * scb, db = t.numel * dcb;
+        const void *sv = src == mdq::ST_P4 ? nullptr : t.exp_avg_sq;
+        const void *dv = dst == mdq::ST_P4 ? nullptr : o.exp_avg_sq;
+        if (ranges_overlap(t.exp_avg, sb, o.exp_avg, db) || (sv && ranges_overlap(sv, sb, o.exp_avg, db)) ||
+            (dv && ranges_overlap(t.exp_avg, sb, dv, db)) || (sv && dv && ranges_overlap(sv, sb, dv, db)))
+            return fail(STQ_ERR_INVALID, "%ssource and destination codes overlap", at.c_str());
+        d.out_m = o.exp_avg;
+        d.out_v = dst == mdq::ST_P4 ? nullptr : o.exp_avg_sq;
+        d.code_m = t.exp_avg;
+        d.code_v = src == mdq::ST_P4 ? nullptr : t.exp_avg_sq;
+        if (!(is_aligned(d.code_m, sca) && (src == mdq::ST_P4 || is_aligned(d.code_v, sca))))
+            d.flags &= ~mdq::DF_ALIGNED;
+        d.tile_begin = tiles;
+        tiles += (t.numel + te - 1) / te;
+        d.tile_end = tiles;
+        descs.push_back(d);
+    }
+    if (descs.empty()) return STQ_OK;
+    if (tiles > 0x7fffffffLL)
+        return fail(STQ_ERR_INVALID, "too many tiles in one call (%lld); split the tensor list", (long long)tiles);
+    return upload_and_launch(descs, src, dst, grad_dt, log2b, rounding == STQ_ROUND_STOCHASTIC, tiles,
                              reinterpret_cast<unsigned long long *>(prof), seed,
                              reinterpret_cast<hipStream_t>(stream));
 }
@@ -480,6 +582,15 @@ int stq_multi_tensor_mdq_adamw(const stq_tensor *tensors, int n_tensors, int gra
 {
     return run(tensors, n_tensors, grad_dtype, exp_avg_dtype, exp_avg_sq_dtype, block_size, rounding, seed,
                profile_cycles, profile_numel, stream);
+}
+
+int stq_multi_tensor_mdq_adamw_restore(const stq_tensor *tensors, const stq_code_out *out, int n_tensors,
+                                       int grad_dtype, int src_storage, int dst_storage, int block_size,
+                                       int rounding, uint64_t seed, int64_t *profile_cycles,
+                                       int64_t profile_numel, void *stream)
+{
+    return run_restore(tensors, out, n_tensors, grad_dtype, src_storage, dst_storage, block_size, rounding, seed,
+                       profile_cycles, profile_numel, stream);
 }
 
 int stq_multi_tensor_grad_stats(const void *const *grads, const int64_t *numels, int n_tensors,

@@ -40,6 +40,10 @@ struct alignas(16) MdqDesc {
     uint32_t step;
     uint32_t tensor_id;
     uint32_t flags;
+    // Destination codes of a storage-changing step (the source codes are
+    // code_m / code_v); unused when the storage stays.
+    void *out_m;
+    void *out_v;
 };
 
 static_assert(sizeof(MdqDesc) % 16 == 0, "descriptor must stay 16-byte sized");

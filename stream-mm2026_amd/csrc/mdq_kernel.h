@@ -68,8 +68,11 @@ __device__ __forceinline__ T ld_g(const void *a) { return *(const MDQ_GLOBAL T *
 template <class T>
 __device__ __forceinline__ void st_g(T v, void *a) { *(MDQ_GLOBAL T *)a = v; }
 
-// Offset inside the quant block of lane j's element e.
-template <int ST, int LOG2B>
+constexpr bool one_byte_codes(int st) { return st == ST_P4 || st == ST_S8; }
+
+// Element layout of a tile whose codes are read in storage SRC and written in
+// storage DST (the same storage except on a storage-changing step).
+template <int SRC, int DST, int LOG2B>
 constexpr bool paired_codes()
 {
     // 1-byte codes (packed 4-bit, or int8 + uint8), 8, 16 or 32 lanes per block: each lane
@@ -77,24 +80,27 @@ constexpr bool paired_codes()
     // instruction) and swaps half of them with lane j ^ LPB/2, so the lane's quads are
     // k*LPB + pi(j) with pi(j) = 2 (j mod LPB/2) + j div LPB/2 for every array.  LLaMA set,
     // same-box A/B against 4-byte quad accesses: packed 4-bit -3.4 %, int8 + uint8 -6 %.
-    return (ST == ST_P4 || ST == ST_S8) && (Cfg<LOG2B>::LPB == 8 || Cfg<LOG2B>::LPB == 16 || Cfg<LOG2B>::LPB == 32);
+    // Wider codes on the other side of a storage change move as 4-element quads at the
+    // same permuted quad positions.
+    return (one_byte_codes(SRC) || one_byte_codes(DST)) &&
+           (Cfg<LOG2B>::LPB == 8 || Cfg<LOG2B>::LPB == 16 || Cfg<LOG2B>::LPB == 32);
 }
 
 // Quad k (0 .. QPL-1) of lane j within its quant block.
-template <int ST, int LOG2B>
+template <bool PAIRED, int LOG2B>
 __device__ __forceinline__ int lane_quad(int j, int k)
 {
     constexpr int LPB = Cfg<LOG2B>::LPB, H = LPB / 2;
-    if constexpr (paired_codes<ST, LOG2B>()) return k * LPB + 2 * (j % H) + j / H;
+    if constexpr (PAIRED) return k * LPB + 2 * (j % H) + j / H;
     else return j + k * LPB;
 }
 
 // Offset within the quant block of the lane's element e.
-template <int ST, int LOG2B>
+template <bool PAIRED, int LOG2B>
 __device__ __forceinline__ int elem_off(int j, int e)
 {
     using C = Cfg<LOG2B>;
-    if constexpr (C::QPL > 0) return 4 * lane_quad<ST, LOG2B>(j, e >> 2) + (e & 3);
+    if constexpr (C::QPL > 0) return 4 * lane_quad<PAIRED, LOG2B>(j, e >> 2) + (e & 3);
     else return e;
 }
 
@@ -389,18 +395,49 @@ struct ProfAcc {
     unsigned long long c[5];
 };
 
+constexpr int code_size(int st) { return st == ST_S16 ? 2 : st == ST_S32 ? 4 : 1; }
+
 // The descriptor with its element pointers advanced to element `off`
 // (workgroup-uniform, so the copies live in scalar registers).
-template <int ST, int GT>
+template <int SRC, int DST, int GT>
 __device__ __forceinline__ MdqDesc tile_view(const MdqDesc &d, int64_t off)
 {
     MdqDesc t = d;
     t.p = d.p + off;
     t.g = static_cast<const char *>(d.g) + off * (GT == GT_F32 ? 4 : 2);
-    constexpr int cb = ST == ST_P4 ? 1 : ST == ST_S8 ? 1 : ST == ST_S16 ? 2 : 4;
-    t.code_m = static_cast<char *>(d.code_m) + off * cb;
-    if constexpr (ST != ST_P4) t.code_v = static_cast<char *>(d.code_v) + off * cb;
+    t.code_m = static_cast<char *>(d.code_m) + off * code_size(SRC);
+    if constexpr (SRC != ST_P4) t.code_v = static_cast<char *>(d.code_v) + off * code_size(SRC);
+    if constexpr (SRC != DST) {
+        t.out_m = static_cast<char *>(d.out_m) + off * code_size(DST);
+        if constexpr (DST != ST_P4) t.out_v = static_cast<char *>(d.out_v) + off * code_size(DST);
+    }
     return t;
+}
+
+// The view the new codes are stored through: the descriptor itself, or on a
+// storage-changing step one whose code pointers are the destination's.
+template <int SRC, int DST>
+__device__ __forceinline__ MdqDesc out_view(const MdqDesc &d)
+{
+    MdqDesc t = d;
+    if constexpr (SRC != DST) {
+        t.code_m = d.out_m;
+        t.code_v = d.out_v;
+    }
+    return t;
+}
+
+// A storage-changing step first re-stores the old codes as the reference's
+// alignment for the new width does (stquant_opt_simple.py:140-173): clamped to
+// int8 / uint8 for widths up to 8 bits (destination P4 or S8), to int16 /
+// uint16 for 16 bits, unchanged for 32; the old scales are kept.  Only int16
+// and int32 sources can fall outside those ranges.
+template <int SRC, int DST>
+constexpr bool narrows_codes()
+{
+    constexpr int src_bits = SRC == ST_S16 ? 16 : SRC == ST_S32 ? 32 : 8;
+    constexpr int dst_bits = DST == ST_S16 ? 16 : DST == ST_S32 ? 32 : 8;
+    return src_bits > dst_bits;
 }
 
 // Dequantised m from its stored code.  Packed nibbles hold mu = q + 8;
@@ -417,14 +454,15 @@ __device__ __forceinline__ float dequant_m(float code, float sm, float neg8sm)
 // FULL: every element of the tile lies inside the tensor and all pointers are
 // 16-byte aligned, so vector accesses are used; otherwise every access is
 // guarded by idx < numel.
-template <int ST, int GT, int LOG2B, bool SR, bool FULL>
+template <int SRC, int DST, int GT, int LOG2B, bool SR, bool FULL>
 __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int lane, int wave,
                                               float *lut, int32_t *xw, unsigned long long seed,
                                               bool prof_on, ProfAcc &pa)
 {
     using C = Cfg<LOG2B>;
     constexpr int B = C::B, EPL = C::EPL, LPB = C::LPB;
-    constexpr bool USE_LUT = (ST == ST_P4) && B >= 32;
+    constexpr bool USE_LUT = (SRC == ST_P4) && B >= 32;
+    constexpr bool PAIRED = paired_codes<SRC, DST, LOG2B>();
 
     unsigned long long t0 = 0;
     if (prof_on) t0 = clock64();
@@ -461,29 +499,39 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
     const int64_t tbase = tl * C::TILE;
     const uint32_t lbase = (uint32_t)bi * B;
     if constexpr (FULL && C::QPL > 0) {
-        const MdqDesc dt = tile_view<ST, GT>(d, tbase);
+        const MdqDesc dt = tile_view<SRC, DST, GT>(d, tbase);
 #pragma unroll
         for (int k = 0; k < C::QPL; ++k) {
-            const uint32_t i = lbase + 4 * lane_quad<ST, LOG2B>(j, k);
+            const uint32_t i = lbase + 4 * lane_quad<PAIRED, LOG2B>(j, k);
             vf4 p4 = ld_nt<vf4>(dt.p + i);
             pv[4 * k + 0] = p4.x; pv[4 * k + 1] = p4.y; pv[4 * k + 2] = p4.z; pv[4 * k + 3] = p4.w;
             GradIO<GT>::load4(dt.g, i, gv + 4 * k);
-            if constexpr (!paired_codes<ST, LOG2B>()) CodeIO<ST>::load4(dt, i, mc + 4 * k, vc + 4 * k);
+            if constexpr (!(PAIRED && one_byte_codes(SRC))) CodeIO<SRC>::load4(dt, i, mc + 4 * k, vc + 4 * k);
         }
-        if constexpr (paired_codes<ST, LOG2B>()) CodeIO<ST>::template load8<LPB / 2>(dt, lbase, j, mc, vc);
+        if constexpr (PAIRED && one_byte_codes(SRC)) CodeIO<SRC>::template load8<LPB / 2>(dt, lbase, j, mc, vc);
 #pragma unroll
         for (int e = 0; e < EPL; ++e) ok[e] = true;
     } else {
 #pragma unroll
         for (int e = 0; e < EPL; ++e) {
-            const int64_t i = base + elem_off<ST, LOG2B>(j, e);
+            const int64_t i = base + elem_off<PAIRED, LOG2B>(j, e);
             ok[e] = FULL || i < n;
             pv[e] = 0.0f; gv[e] = 0.0f; mc[e] = 0.0f; vc[e] = 0;
             if (ok[e]) {
                 pv[e] = ld_g<float>(d.p + i);
                 gv[e] = GradIO<GT>::load1(d.g, i);
-                CodeIO<ST>::load1(d, i, mc[e], vc[e]);
+                CodeIO<SRC>::load1(d, i, mc[e], vc[e]);
             }
+        }
+    }
+    if constexpr (narrows_codes<SRC, DST>()) {
+        constexpr float lo = DST == ST_S16 ? -32768.0f : -128.0f;
+        constexpr float hi = DST == ST_S16 ? 32767.0f : 127.0f;
+        constexpr uint32_t vhi = DST == ST_S16 ? 65535u : 255u;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+            mc[e] = __builtin_amdgcn_fmed3f(mc[e], lo, hi);    // int32 -> float is monotonic
+            vc[e] = vc[e] < vhi ? vc[e] : vhi;
         }
     }
 
@@ -513,7 +561,7 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
     float m[EPL], v[EPL], lv[EPL];
 #pragma unroll
     for (int e = 0; e < EPL; ++e) {
-        const float m0 = dequant_m<ST>(mc[e], sm, neg8sm);
+        const float m0 = dequant_m<SRC>(mc[e], sm, neg8sm);
         float v0;
         if constexpr (USE_LUT) v0 = lut[bi * 16 + vc[e]];
         else v0 = mdq_expf(fma_((float)vc[e], sv, vmin));
@@ -624,7 +672,7 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
     int32_t qmi[EPL];
     uint32_t qvi[EPL];
     float pk[EPL];                                            // packed byte values (P4)
-    const bool wide = (ST == ST_S32) && d.bits > 16;          // uniform per tensor
+    const bool wide = (DST == ST_S32) && d.bits > 16;         // uniform per tensor
     if (!wide) {
         float qmf[EPL], qvf[EPL];
         if constexpr (SR) {
@@ -636,7 +684,7 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
             if constexpr (C::QPL > 0) {
 #pragma unroll
                 for (int k = 0; k < C::QPL; ++k) {
-                    const uint64_t q = (uint64_t)((base >> 2) + lane_quad<ST, LOG2B>(j, k));
+                    const uint64_t q = (uint64_t)((base >> 2) + lane_quad<PAIRED, LOG2B>(j, k));
                     U4 r = mdq_philox4x32_10(U4{(uint32_t)q, (uint32_t)(q >> 32), d.tensor_id, d.step},
                                              (uint32_t)seed, (uint32_t)(seed >> 32));
                     const uint32_t w[4] = {r.x, r.y, r.z, r.w};
@@ -747,7 +795,7 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
         for (int e = 0; e < EPL; ++e) {
             const float qm = __builtin_amdgcn_fmed3f(qmf[e], -d.qm, d.qm - 1.0f);
             const float qv = __builtin_amdgcn_fmed3f(qvf[e], 0.0f, d.qvf);
-            if constexpr (ST == ST_P4) {
+            if constexpr (DST == ST_P4) {
                 pk[e] = fma_(qv, 16.0f, qm + 8.0f);           // (v << 4) | (m + 8), exact
             } else {
                 qmi[e] = (int32_t)qm;
@@ -781,28 +829,30 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
     }
 
     if constexpr (FULL && C::QPL > 0) {
-        const MdqDesc dt = tile_view<ST, GT>(d, tbase);
+        const MdqDesc dt = tile_view<SRC, DST, GT>(d, tbase);
+        const MdqDesc ot = out_view<SRC, DST>(dt);
 #pragma unroll
         for (int k = 0; k < C::QPL; ++k) {
-            const uint32_t i = lbase + 4 * lane_quad<ST, LOG2B>(j, k);
-            if constexpr (!paired_codes<ST, LOG2B>()) {
-                if constexpr (ST == ST_P4) CodeIO<ST>::store4f(dt, i, pk + 4 * k);
-                else CodeIO<ST>::store4(dt, i, qmi + 4 * k, qvi + 4 * k);
+            const uint32_t i = lbase + 4 * lane_quad<PAIRED, LOG2B>(j, k);
+            if constexpr (!(PAIRED && one_byte_codes(DST))) {
+                if constexpr (DST == ST_P4) CodeIO<DST>::store4f(ot, i, pk + 4 * k);
+                else CodeIO<DST>::store4(ot, i, qmi + 4 * k, qvi + 4 * k);
             }
             vf4 o = {pv[4 * k + 0], pv[4 * k + 1], pv[4 * k + 2], pv[4 * k + 3]};
             st_nt<vf4>(o, dt.p + i);
         }
-        if constexpr (paired_codes<ST, LOG2B>()) {
-            if constexpr (ST == ST_P4) CodeIO<ST>::template store8f<LPB / 2>(dt, lbase, j, pk);
-            else CodeIO<ST>::template store8<LPB / 2>(dt, lbase, j, qmi, qvi);
+        if constexpr (PAIRED && one_byte_codes(DST)) {
+            if constexpr (DST == ST_P4) CodeIO<DST>::template store8f<LPB / 2>(ot, lbase, j, pk);
+            else CodeIO<DST>::template store8<LPB / 2>(ot, lbase, j, qmi, qvi);
         }
     } else {
+        const MdqDesc od = out_view<SRC, DST>(d);
 #pragma unroll
         for (int e = 0; e < EPL; ++e) {
             if (ok[e]) {
-                const int64_t i = base + elem_off<ST, LOG2B>(j, e);
-                if constexpr (ST == ST_P4) CodeIO<ST>::store1f(d, i, pk[e]);
-                else CodeIO<ST>::store1(d, i, qmi[e], qvi[e]);
+                const int64_t i = base + elem_off<PAIRED, LOG2B>(j, e);
+                if constexpr (DST == ST_P4) CodeIO<DST>::store1f(od, i, pk[e]);
+                else CodeIO<DST>::store1(od, i, qmi[e], qvi[e]);
                 st_g<float>(pv[e], d.p + i);
             }
         }
@@ -818,7 +868,7 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
 // tile starts, so the ~log2(n_desc) dependent scalar loads hit a few cache
 // lines).  Profiling (prof != null) samples every 64th tile; only the phase
 // ratios of the cycle sums are meaningful.
-template <int ST, int GT, int LOG2B, bool SR>
+template <int SRC, int DST, int GT, int LOG2B, bool SR>
 __global__ __launch_bounds__(Cfg<LOG2B>::THREADS) void mdq_step_kernel(const MdqDesc *__restrict__ descs,
                                                                       const long long *__restrict__ tile_begin,
                                                                       int n_desc,
@@ -826,7 +876,7 @@ __global__ __launch_bounds__(Cfg<LOG2B>::THREADS) void mdq_step_kernel(const Mdq
                                                                       unsigned long long seed)
 {
     using C = Cfg<LOG2B>;
-    constexpr bool USE_LUT = (ST == ST_P4) && C::B >= 32;
+    constexpr bool USE_LUT = (SRC == ST_P4) && C::B >= 32;
     __shared__ float lut_s[USE_LUT ? C::TB * 16 : 1];
     __shared__ int32_t xw_s[6];
     const int lane = threadIdx.x & 63;
@@ -845,8 +895,8 @@ __global__ __launch_bounds__(Cfg<LOG2B>::THREADS) void mdq_step_kernel(const Mdq
     const bool prof_on = prof != nullptr && (tile & 63) == 0;
     ProfAcc pa = {{0, 0, 0, 0, 0}};
     const bool full = (d.flags & DF_ALIGNED) && (tl + 1) * C::TILE <= d.numel;
-    if (full) mdq_step_tile<ST, GT, LOG2B, SR, true>(d, tl, lane, wave, lut_s, xw_s, seed, prof_on, pa);
-    else mdq_step_tile<ST, GT, LOG2B, SR, false>(d, tl, lane, wave, lut_s, xw_s, seed, prof_on, pa);
+    if (full) mdq_step_tile<SRC, DST, GT, LOG2B, SR, true>(d, tl, lane, wave, lut_s, xw_s, seed, prof_on, pa);
+    else mdq_step_tile<SRC, DST, GT, LOG2B, SR, false>(d, tl, lane, wave, lut_s, xw_s, seed, prof_on, pa);
     if (prof_on && threadIdx.x == 0) {
 #pragma unroll
         for (int s = 0; s < 5; ++s) atomicAdd(prof + s, pa.c[s]);

@@ -240,6 +240,46 @@ def multi_tensor_step(entries: Sequence[TensorState], block_size: int, *,
     MultiTensorPlan(entries, block_size, rounding=rounding, seed=seed).run(profile_cycles)
 
 
+# stq_code_out: destination code pointers and sizes of one tensor of a storage-changing step
+STQ_CODE_OUT_DTYPE = np.dtype([("exp_avg", np.uint64), ("exp_avg_sq", np.uint64), ("exp_avg_numel", np.int64),
+                               ("exp_avg_sq_numel", np.int64)])
+# block sizes with storage-changing step kernels (stq_multi_tensor_mdq_adamw_restore)
+RESTORE_BLOCK_SIZES = (64, 128, 256)
+
+
+def multi_tensor_restore(entries: Sequence[TensorState], outs, block_size: int, *,
+                         rounding=ROUND_NEAREST, seed: int = 0,
+                         profile_cycles: Optional[torch.Tensor] = None) -> None:
+    """One launch of a step that changes the code storage: each entry's codes are read from
+    ``exp_avg`` / ``exp_avg_sq`` (one source storage for all entries) and its new codes written
+    to ``outs[i] = (exp_avg, exp_avg_sq)`` (one destination storage), as MDQAdamWSimple's
+    align -> kernel -> pack route for a changed bit width (stquant_opt_simple.py:231-280)."""
+    entries, outs = list(entries), list(outs)
+    if len(entries) != len(outs):
+        raise RuntimeError("multi_tensor_restore: one destination per tensor")
+    if not entries:
+        return
+    src = storage_of(entries[0].exp_avg, entries[0].exp_avg_sq)
+    dst = storage_of(*outs[0])
+    out = np.zeros(len(entries), dtype=STQ_CODE_OUT_DTYPE)
+    dev = entries[0].p.device
+    for k, (e, (m, v)) in enumerate(zip(entries, outs)):
+        if storage_of(e.exp_avg, e.exp_avg_sq) != src or storage_of(m, v) != dst:
+            raise RuntimeError("multi_tensor_restore: one source and one destination storage per call")
+        for t in (e.exp_avg, e.exp_avg_sq, m, v):
+            if t.numel() and (t.device != dev or not t.is_contiguous()):
+                raise RuntimeError("multi_tensor_restore: code tensors must be contiguous and on the params' device")
+        out[k] = (m.data_ptr() if m.numel() else 0, v.data_ptr() if v.numel() else 0, m.numel(), v.numel())
+    arr, (gdt, _eadt, _easqdt) = _pack_entries(entries)
+    prof_ptr, prof_n = _profile_args(profile_cycles)
+    with torch.cuda.device(dev):
+        rc = lib().stq_multi_tensor_mdq_adamw_restore(
+            arr.ctypes.data_as(ctypes.POINTER(StqTensor)), out.ctypes.data, len(entries), gdt, src, dst,
+            int(block_size), rounding_code(rounding), int(seed) & 0xFFFFFFFFFFFFFFFF, prof_ptr, prof_n,
+            _capi.stream_handle(dev))
+    check(rc)
+
+
 def grad_stats(grads: Sequence[torch.Tensor], out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Per-tensor ``(sqrt(mean g^2), std(g) / (mean|g| + 1e-12), mean g^2)`` as a float32
     ``[len(grads), 3]`` device tensor, from one multi-tensor launch per grad dtype (fp64 sums,

@@ -34,6 +34,7 @@ DTYPE_CODES = {
 EXPORTED_SYMBOLS = (
     "stq_fused_mdq_adamw",
     "stq_multi_tensor_mdq_adamw",
+    "stq_multi_tensor_mdq_adamw_restore",
     "stq_multi_tensor_grad_stats",
     "stq_multi_tensor_convert_codes",
     "stq_last_error",
@@ -106,6 +107,9 @@ def lib() -> ctypes.CDLL:
     L.stq_multi_tensor_mdq_adamw.argtypes = [
         ctypes.POINTER(StqTensor), i32, i32, i32, i32, i32, i32, u64, vp, i64, vp]
     L.stq_multi_tensor_mdq_adamw.restype = ctypes.c_int
+    L.stq_multi_tensor_mdq_adamw_restore.argtypes = [
+        ctypes.POINTER(StqTensor), vp, i32, i32, i32, i32, i32, i32, u64, vp, i64, vp]
+    L.stq_multi_tensor_mdq_adamw_restore.restype = ctypes.c_int
     L.stq_multi_tensor_convert_codes.argtypes = [vp, i32, vp]
     L.stq_multi_tensor_convert_codes.restype = ctypes.c_int
     L.stq_multi_tensor_grad_stats.argtypes = [vp, vp, i32, i32, vp, vp]

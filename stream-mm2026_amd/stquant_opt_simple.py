@@ -91,6 +91,10 @@ class MDQAdamWSimple(Optimizer):
     # storage changes of CUDA tensors in one conversion launch per step; False keeps the
     # reference's per-tensor torch passes (same results)
     _device_transitions = True
+    # with device transitions: a tensor whose storage changes is stepped by a kernel that reads
+    # the old storage and writes the new one (block sizes 64 / 128 / 256), instead of convert ->
+    # step -> pack; False keeps the separate passes (same results)
+    _fused_transitions = True
 
     def add_param_group(self, param_group):
         self.__dict__["_steady"] = None
@@ -328,7 +332,7 @@ class MDQAdamWSimple(Optimizer):
             return False
         pending = self.__dict__.get("_pending_align")
         if pending is not None and state["exp_avg"].is_cuda:
-            pending.append((state, bits))              # one conversion launch for all (_flush_align)
+            pending.append((p, group, state, bits))    # one launch for all (_flush_align)
         else:
             self._align_momentum_storage(state, bits)
         return True
@@ -351,6 +355,18 @@ class MDQAdamWSimple(Optimizer):
             return mdq_hip.STORE_S16
         return mdq_hip.STORE_S8
 
+    @classmethod
+    def _final_storage(cls, bits: int):
+        """The code storage a step at ``bits`` leaves (align, kernel, pack: :140-219), or None
+        for widths the storage cannot hold (17..31 bits go to int16 there)."""
+        if bits == 4:
+            return mdq_hip.STORE_P4
+        if 1 <= bits <= 16 or bits == 32:
+            return cls._aligned_storage(bits)
+        return None
+
+    _RESTORE_GRAD_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
+
     @staticmethod
     def _convert_states(moves):
         """Re-store the codes of ``[(state, dst_storage)]`` with one conversion launch."""
@@ -366,19 +382,57 @@ class MDQAdamWSimple(Optimizer):
 
     def _flush_align(self):
         """Device version of _align_momentum_storage for all deferred tensors: the same value map
-        (unpack nibbles, widen, or clamp to the narrower range; :140-198) in one launch."""
+        (unpack nibbles, widen, or clamp to the narrower range; :140-198) in one launch.
+
+        Tensors that a storage-changing kernel can step (``_fused_transitions``) are not
+        converted: they get destination codes in their final storage and are collected in
+        ``self._restores`` for ``_run_restores``."""
         pending, self._pending_align = self.__dict__.get("_pending_align") or [], None
         moves = []
-        for state, bits in pending:
+        restores = {}
+        for p, group, state, bits in pending:
             if state["exp_avg"].numel() == 0:          # the reference's dtype rules for empty tensors
                 self._align_momentum_storage(state, bits)
                 continue
             src = mdq_hip.storage_of(state["exp_avg"], state["exp_avg_sq"])
+            fin = self._final_storage(bits)
+            if (self._fused_transitions and fin is not None and fin != src
+                    and min(int(group["block_size"]), 1024) in mdq_hip.RESTORE_BLOCK_SIZES
+                    and p.grad.dtype in self._RESTORE_GRAD_DTYPES):
+                restores[id(p)] = (p, group, state, mdq_hip.empty_codes(state["exp_avg"], fin))
+                continue
             dst = self._aligned_storage(bits)
             if src != dst:
                 moves.append((state, dst))
         if moves:
             self._convert_states(moves)
+        self._restores = restores
+
+    def _run_restores(self, restores):
+        """Storage-changing steps: one launch per (device, source storage, destination storage,
+        grad dtype, block size, rounding, seed), then the new codes replace the old ones."""
+        buckets = OrderedDict()
+        ids = self._tensor_ids
+        for p, group, state, out in restores:
+            grad = p.grad if p.grad.is_contiguous() else p.grad.contiguous()
+            key = (p.device, mdq_hip.storage_of(state["exp_avg"], state["exp_avg_sq"]),
+                   mdq_hip.storage_of(*out), grad.dtype, min(int(group["block_size"]), 1024),
+                   mdq_hip.rounding_code(group.get("rounding", "nearest")), int(group.get("seed", 0) or 0))
+            buckets.setdefault(key, []).append((p, group, state, out, grad))
+        for key, lst in buckets.items():
+            dev, bsz, rnd, seed = key[0], key[4], key[5], key[6]
+            entries = [mdq_hip.TensorState(
+                p=p, grad=gr, exp_avg=st["exp_avg"], exp_avg_sq=st["exp_avg_sq"], scale_m=st["scale_m"],
+                scale_v=st["scale_v"], v_min=st["v_min"], step=st["step"], bits=int(st["current_bit"]),
+                lr=g["lr"], beta1=g["betas"][0], beta2=g["betas"][1], eps=g["eps"],
+                weight_decay=g["weight_decay"], tensor_id=ids.get(p, 0)) for p, g, st, _o, gr in lst]
+            prof = None
+            if self.sync_timing and self._kernel_profile_buf is not None and self._kernel_profile_device == dev:
+                prof = self._kernel_profile_buf
+            mdq_hip.multi_tensor_restore(entries, [o for _p, _g, _st, o, _gr in lst], bsz, rounding=rnd,
+                                         seed=seed, profile_cycles=prof)
+            for _p, _g, st, (nm, nv), _gr in lst:
+                st["exp_avg"], st["exp_avg_sq"] = nm, nv
 
     def _flush_pack(self):
         """Device version of _pack_momentum_storage after the step: 4-bit tensors in int8/uint8
@@ -769,7 +823,13 @@ class MDQAdamWSimple(Optimizer):
         if self.sync_timing:
             self._sync_device(dev)
         tk0 = time.perf_counter()
-        runs = self._run_kernels(params_with_grad)
+        restores = self.__dict__.pop("_restores", None) or {}
+        if restores:
+            steady = [(p, g) for p, g in params_with_grad if id(p) not in restores]
+            runs = self._run_kernels(steady) if steady else []
+            self._run_restores(list(restores.values()))
+        else:
+            runs = self._run_kernels(params_with_grad)
         if self.sync_timing:
             self._sync_device(dev)
         kernel_ms = (time.perf_counter() - tk0) * 1000.0
@@ -777,7 +837,7 @@ class MDQAdamWSimple(Optimizer):
         self._pending_pack = [] if self._device_transitions else None
         try:
             for (p, _g), rp in zip(params_with_grad, repack):
-                if rp:
+                if rp and id(p) not in restores:
                     self._finish_update(p)
         finally:
             self._flush_pack()

@@ -92,3 +92,51 @@ def test_multi_tensor_rejects_mixed_storage():
     # tensor 0 is packed4 (empty v codes), tensor 1 would be uint8+uint8: not a valid pair
     rc = L.stq_multi_tensor_mdq_adamw(arr, 2, 0, 3, 3, 128, 0, 0, None, 0, None)
     assert rc == _capi.STQ_ERR_INVALID and "MDQ: state must be packed4" in err()
+
+
+class StqCodeOut(ctypes.Structure):
+    _fields_ = [("exp_avg", ctypes.c_void_p), ("exp_avg_sq", ctypes.c_void_p),
+                ("exp_avg_numel", ctypes.c_int64), ("exp_avg_sq_numel", ctypes.c_int64)]
+
+
+def call_restore(src=2, dst=0, bits=4, block=128, numel=256, src_m=FAKE, src_v=FAKE + 4096, dst_m=FAKE + 8192,
+                 dst_v=None, src_n=None, dst_n=None):
+    """stq_multi_tensor_mdq_adamw_restore on one tensor of fake (never dereferenced) pointers."""
+    t = (_capi.StqTensor * 1)()
+    s = t[0]
+    s.p, s.grad, s.scale_m, s.scale_v, s.v_min = FAKE, FAKE, FAKE, FAKE, FAKE
+    s.exp_avg, s.exp_avg_sq = src_m, (None if src == 0 else src_v)
+    s.numel = s.grad_numel = numel
+    s.exp_avg_numel = numel if src_n is None else src_n
+    s.exp_avg_sq_numel = 0 if src == 0 else (numel if src_n is None else src_n)
+    s.scale_m_numel = s.scale_v_numel = s.v_min_numel = (numel + block - 1) // block
+    s.beta1, s.beta2, s.lr, s.weight_decay, s.eps = 0.9, 0.999, 1e-3, 0.0, 1e-8
+    s.step, s.bits = 1, bits
+    o = (StqCodeOut * 1)()
+    o[0].exp_avg, o[0].exp_avg_sq = dst_m, dst_v
+    o[0].exp_avg_numel = numel if dst_n is None else dst_n
+    o[0].exp_avg_sq_numel = 0 if dst == 0 else (numel if dst_n is None else dst_n)
+    return mdq_hip.lib().stq_multi_tensor_mdq_adamw_restore(t, o, 1, 0, src, dst, block, 0, 0, None, 0, None)
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(src=0, dst=0), "source and destination storage are the same"),
+    (dict(block=512), "block size must be 64, 128 or 256, got 512"),
+    (dict(block=32), "block size must be 64, 128 or 256, got 32"),
+    (dict(src=1, dst=2, bits=4, dst_v=FAKE + 65536), "bits=4 is not stored in destination storage 2"),
+    (dict(dst=1, bits=16, dst_v=FAKE + 65536), "bits=16 is not stored in destination storage 1"),
+    (dict(dst=3, src=1, bits=24, dst_v=FAKE + 65536), "bits=24 is not stored in destination storage 3"),
+    (dict(src_n=100), "source codes must hold numel (256) codes"),
+    (dict(dst_n=100), "packed4: exp_avg numel must match parameters"),
+    (dict(dst_m=FAKE + 4096 + 100), "source and destination codes overlap"),
+    (dict(src=5), "storage must be STQ_STORE_P4 .. STQ_STORE_S32"),
+])
+def test_restore_argument_errors(kw, msg):
+    assert call_restore(**kw) == _capi.STQ_ERR_INVALID
+    assert msg in err()
+
+
+def test_restore_empty_list_is_a_no_op():
+    L = mdq_hip.lib()
+    assert L.stq_multi_tensor_mdq_adamw_restore(None, None, 0, 0, 2, 0, 128, 0, 0, None, 0, None) == _capi.STQ_OK
+    assert call_restore(numel=0) == _capi.STQ_OK
