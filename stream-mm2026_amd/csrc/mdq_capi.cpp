@@ -166,7 +166,8 @@ struct Slot {
     char *dev = nullptr;
     char *host = nullptr;
     size_t cap = 0;   // bytes
-    hipEvent_t done = nullptr;
+    hipEvent_t done = nullptr;     // recorded behind the slot's last launch
+    hipEvent_t copied = nullptr;   // recorded behind the slot's last upload on the copy stream
     bool pending = false;
 };
 
@@ -174,6 +175,7 @@ struct DevCtx {
     std::mutex mu;
     int cus = 0;
     int next = 0;
+    hipStream_t copy_stream = nullptr;   // descriptor uploads (default priority)
     Slot slots[8];
 };
 
@@ -225,8 +227,45 @@ int take_slot(DevCtx *ctx, size_t need, Slot **out)
         e = hipEventCreateWithFlags(&s.done, hipEventDisableTiming);
         if (e != hipSuccess) return hip_fail(e, "hipEventCreate");
     }
+    if (!s.copied) {
+        e = hipEventCreateWithFlags(&s.copied, hipEventDisableTiming);
+        if (e != hipSuccess) return hip_fail(e, "hipEventCreate");
+    }
     *out = &s;
     return STQ_OK;
+}
+
+// Copies the first `bytes` of the slot's staging buffer to its device buffer
+// so that work queued next on `stream` sees them.  The copy goes on the
+// device's copy stream and `stream` waits for it: a copy queued on `stream`
+// itself would start only after the previous kernel there has finished, and
+// the next kernel would wait for it, leaving the GPU idle between
+// back-to-back steps.  The slot is free (take_slot waited for its last
+// launch), so the copy cannot overwrite descriptors still in use.  A stream
+// under graph capture gets the copy on itself.  Called with ctx->mu held.
+int upload(DevCtx *ctx, Slot &s, size_t bytes, hipStream_t stream)
+{
+    hipError_t e;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(stream, &cs);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
+    if (cs == hipStreamCaptureStatusNone && !ctx->copy_stream) {
+        e = hipStreamCreateWithFlags(&ctx->copy_stream, hipStreamNonBlocking);
+        if (e != hipSuccess) {
+            ctx->copy_stream = nullptr;
+            return hip_fail(e, "hipStreamCreate(descriptor copies)");
+        }
+    }
+    if (cs != hipStreamCaptureStatusNone) {
+        e = hipMemcpyAsync(s.dev, s.host, bytes, hipMemcpyHostToDevice, stream);
+        return e == hipSuccess ? STQ_OK : hip_fail(e, "hipMemcpyAsync(descriptors)");
+    }
+    e = hipMemcpyAsync(s.dev, s.host, bytes, hipMemcpyHostToDevice, ctx->copy_stream);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(descriptors)");
+    e = hipEventRecord(s.copied, ctx->copy_stream);
+    if (e != hipSuccess) return hip_fail(e, "hipEventRecord");
+    e = hipStreamWaitEvent(stream, s.copied, 0);
+    return e == hipSuccess ? STQ_OK : hip_fail(e, "hipStreamWaitEvent");
 }
 
 // Marks the slot busy until the work queued so far on `stream` completes.
@@ -258,8 +297,9 @@ int upload_and_launch(const std::vector<MdqDesc> &descs, int src_storage, int st
     std::memcpy(s.host, descs.data(), n * sizeof(MdqDesc));
     long long *tb = reinterpret_cast<long long *>(s.host + n * sizeof(MdqDesc));
     for (size_t i = 0; i < n; ++i) tb[i] = descs[i].tile_begin;
-    hipError_t e = hipMemcpyAsync(s.dev, s.host, need, hipMemcpyHostToDevice, stream);
-    if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(descriptors)");
+    rc = upload(ctx, s, need, stream);
+    if (rc != STQ_OK) return rc;
+    hipError_t e;
 
     const MdqDesc *dd = reinterpret_cast<const MdqDesc *>(s.dev);
     const int nd = (int)n;
@@ -320,8 +360,9 @@ int run_grad_stats(const void *const *grads, const int64_t *numels, int n, int g
     std::memcpy(s->host, d.data(), (size_t)n * sizeof(mdq::StatDesc));
     long long *tb = reinterpret_cast<long long *>(s->host + (size_t)n * sizeof(mdq::StatDesc));
     for (int i = 0; i < n; ++i) tb[i] = d[i].tile_begin;
-    hipError_t e = hipMemcpyAsync(s->dev, s->host, up, hipMemcpyHostToDevice, stream);
-    if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(descriptors)");
+    rc = upload(ctx, *s, up, stream);
+    if (rc != STQ_OK) return rc;
+    hipError_t e;
     const mdq::StatDesc *dd = reinterpret_cast<const mdq::StatDesc *>(s->dev);
     const long long *dtb = reinterpret_cast<const long long *>(s->dev + (size_t)n * sizeof(mdq::StatDesc));
     double *partials = reinterpret_cast<double *>(s->dev + part_off);
@@ -526,8 +567,9 @@ int run_convert(const stq_code_convert *items, int n, hipStream_t stream)
     std::memcpy(s->host, d.data(), m * sizeof(mdq::ConvDesc));
     long long *tb = reinterpret_cast<long long *>(s->host + m * sizeof(mdq::ConvDesc));
     for (size_t i = 0; i < m; ++i) tb[i] = d[i].tile_begin;
-    hipError_t e = hipMemcpyAsync(s->dev, s->host, need, hipMemcpyHostToDevice, stream);
-    if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(descriptors)");
+    rc = upload(ctx, *s, need, stream);
+    if (rc != STQ_OK) return rc;
+    hipError_t e;
     e = mdq::launch_convert(reinterpret_cast<const mdq::ConvDesc *>(s->dev),
                             reinterpret_cast<const long long *>(s->dev + m * sizeof(mdq::ConvDesc)), (int)m,
                             tiles, stream);
