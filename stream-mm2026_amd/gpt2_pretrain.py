@@ -117,17 +117,21 @@ def train(optimizer_name: str = "MDQAdamW-Simple-FusedIO", *, steps: int = 300, 
           batch: int = 8, seq_len: int = 1024, lr: float = 2e-4, bits=4, block_size: int = 128,
           rounding: str = "stochastic", data_seed: int = 1234, model_seed: int = 42, opt_seed: int = 0,
           n_layer: int = 12, n_embd: int = 768, n_head: int = 12, vocab_used: int = VOCAB,
-          device="cuda:0", log_every: int = 0):
+          device="cuda:0", log_every: int = 0, fused_transitions: bool = True):
     """Run ``warmup`` untimed-history steps then ``steps`` measured steps; return the summary.
 
     Tokens are uniform over ``[0, vocab_used)`` (the full vocabulary by default; a smaller range
-    gives a learnable unigram task whose loss falls towards ``log(vocab_used)``)."""
+    gives a learnable unigram task whose loss falls towards ``log(vocab_used)``).  ``bits=None``
+    runs the MDQ score-based bit schedule; ``fused_transitions=False`` steps tensors whose bit
+    width changes with separate conversion passes instead of the storage-changing kernel."""
     dev = torch.device(device)
     model = build_model(dev, n_layer=n_layer, n_embd=n_embd, n_head=n_head, n_positions=seq_len,
                         seed=model_seed)
     opt = build_optimizer(optimizer_name, model, lr, n_layer, batch, bits=bits, block_size=block_size,
                           rounding=rounding, seed=opt_seed)
     is_mdq = optimizer_name.startswith("MDQ")
+    if is_mdq:
+        opt._fused_transitions = fused_transitions
     gen = torch.Generator(device=dev).manual_seed(data_seed)
     torch.manual_seed(model_seed)
     hist = {k: [] for k in ("loss", "forward_ms", "backward_ms", "step_wall_ms", "optimizer_step_ms")}
@@ -136,6 +140,7 @@ def train(optimizer_name: str = "MDQAdamW-Simple-FusedIO", *, steps: int = 300, 
             hist[k] = []
         if optimizer_name == "MDQAdamW-Simple-FusedIO":
             hist["mdq_fused_io_fast_path_ratio"] = []
+            hist["mdq_fused_io_fallback_params"] = []
     sync = torch.cuda.synchronize
     measure_start = None
     torch.cuda.reset_peak_memory_stats(dev)
@@ -171,6 +176,7 @@ def train(optimizer_name: str = "MDQAdamW-Simple-FusedIO", *, steps: int = 300, 
                 hist[hk].append(lt.get(tk, 0.0))
             if "mdq_fused_io_fast_path_ratio" in hist:
                 hist["mdq_fused_io_fast_path_ratio"].append(lt.get("mdq_fused_io_fast_path_ratio", 0.0))
+                hist["mdq_fused_io_fallback_params"].append(lt.get("mdq_fused_io_fallback_params", 0))
         if log_every and (it - warmup + 1) % log_every == 0:
             print(f"[gpt2] {optimizer_name} step {it - warmup + 1}/{steps} loss {hist['loss'][-1]:.4f} "
                   f"step {hist['step_wall_ms'][-1]:.1f} ms opt {hist['optimizer_step_ms'][-1]:.2f} ms",
@@ -184,6 +190,7 @@ def train(optimizer_name: str = "MDQAdamW-Simple-FusedIO", *, steps: int = 300, 
         "Bits": bits if is_mdq else 32,
         "Block_Size": block_size if is_mdq else None,
         "Params": n_params,
+        "Params_Tensors": sum(1 for _ in model.parameters()),
         "Avg_Loss": _avg(hist["loss"]),
         "Final_Loss_Avg10": _avg(hist["loss"][-10:]),
         "Measure_Train_Wall_ms": wall_ms,

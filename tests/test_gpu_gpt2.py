@@ -5,7 +5,10 @@ the oracle per tests/test_gpu_optimizer.py) on identical seeded batches.
 - uniform tokens over the full vocabulary (the config's data): loss curves within 1 %;
 - tokens from the first 256 ids (a learnable unigram task whose loss floor is log 256): every
   optimizer brings the loss from log 50257 + (excess of the random init) to within 0.25 nats of
-  the floor, and the 4-bit runs end within 2 % of fp32 AdamW's final loss."""
+  the floor, and the 4-bit runs end within 2 % of fp32 AdamW's final loss;
+- the MDQ score-based bit schedule (bits change on update steps) with the storage-changing kernel
+  and with separate conversion passes: the same loss curve (up to the run-to-run variation of
+  autograd's atomic accumulations)."""
 import math
 
 import pytest
@@ -46,3 +49,16 @@ def test_learnable_tokens_all_optimizers_learn():
     for k in ("sr", "rn"):
         assert abs(last[k] - last["adamw"]) <= 0.02 * last["adamw"], k
     assert gp.compare_loss_curves(runs["sr"]["History"]["loss"], runs["rn"]["History"]["loss"], 5) <= 0.05
+
+
+def test_default_schedule_fused_transitions_match_separate_passes():
+    kw = dict(bits=None, lr=1e-3, vocab_used=256)
+    a = _run("MDQAdamW-Simple-FusedIO", "nearest", 24, fused_transitions=True, **kw)
+    b = _run("MDQAdamW-Simple-FusedIO", "nearest", 24, fused_transitions=False, **kw)
+    fa, fb = a["History"]["mdq_fused_io_fallback_params"], b["History"]["mdq_fused_io_fallback_params"]
+    print(f"tensors changing storage per step: {fa}", flush=True)
+    # step 1 moves every tensor not scored at 16 bits out of the initial int16 storage
+    assert 0 < fa[0] <= a["Params_Tensors"] and sum(x > 0 for x in fa) >= 2
+    gap = gp.compare_loss_curves(a["History"]["loss"], b["History"]["loss"], window=1)
+    print(f"default schedule: max per-step loss gap fused vs separate {gap:.2e}", flush=True)
+    assert gap <= 2e-3
