@@ -245,12 +245,14 @@ def e2e_gpt2(steps: int, warmup: int, out_path):
     import gpt2_pretrain
 
     runs = {}
-    for key, name, rounding in (("mdq4_stochastic", "MDQAdamW-Simple-FusedIO", "stochastic"),
-                                ("mdq4_nearest", "MDQAdamW-Simple-FusedIO", "nearest"),
-                                ("adamw32", "AdamW-32bit", None)):
+    for key, name, rounding, bits in (("mdq4_stochastic", "MDQAdamW-Simple-FusedIO", "stochastic", 4),
+                                      ("mdq4_nearest", "MDQAdamW-Simple-FusedIO", "nearest", 4),
+                                      ("adamw32", "AdamW-32bit", None, 4),
+                                      # the reference's default: score-based bit widths (MDQ schedule)
+                                      ("mdq_schedule_nearest", "MDQAdamW-Simple-FusedIO", "nearest", None)):
         log(f"gpt2 e2e: {key} ({steps} steps)")
         runs[key] = gpt2_pretrain.train(name, steps=steps, warmup=warmup, rounding=rounding or "nearest",
-                                        log_every=50)
+                                        bits=bits, log_every=50)
     la = runs["mdq4_stochastic"]["History"]["loss"]
     lb = runs["mdq4_nearest"]["History"]["loss"]
     lc = runs["adamw32"]["History"]["loss"]
@@ -265,6 +267,9 @@ def e2e_gpt2(steps: int, warmup: int, out_path):
         "loss_gap_stochastic_vs_adamw32": {
             "max_rel_smoothed10": gpt2_pretrain.compare_loss_curves(la, lc, 10),
             "max_rel_per_step": gpt2_pretrain.compare_loss_curves(la, lc, 1)},
+        "loss_gap_schedule_vs_adamw32": {
+            "max_rel_smoothed10": gpt2_pretrain.compare_loss_curves(runs["mdq_schedule_nearest"]["History"]["loss"], lc, 10),
+            "max_rel_per_step": gpt2_pretrain.compare_loss_curves(runs["mdq_schedule_nearest"]["History"]["loss"], lc, 1)},
         "runs": {k: {kk: vv for kk, vv in v.items() if kk != "History"} for k, v in runs.items()},
     }
     if out_path:

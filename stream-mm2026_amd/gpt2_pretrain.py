@@ -219,6 +219,8 @@ def train(optimizer_name: str = "MDQAdamW-Simple-FusedIO", *, steps: int = 300, 
         })
         if "mdq_fused_io_fast_path_ratio" in hist:
             res["Avg_FusedIO_FastPath_Ratio"] = _avg(hist["mdq_fused_io_fast_path_ratio"])
+        res["Bit_Distribution_Final"] = opt.get_bit_distribution()
+        res["Avg_Bits_Param_Weighted_Final"] = opt.get_avg_bit_param_weighted()
     res["History"] = hist
     return res
 
