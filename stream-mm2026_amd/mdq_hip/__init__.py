@@ -189,6 +189,8 @@ class MultiTensorPlan:
     def run(self, profile_cycles: Optional[torch.Tensor] = None) -> None:
         if self.n == 0:
             return
+        if self.device.type != "cuda":
+            raise RuntimeError("p/grad must be CUDA")
         prof_ptr, prof_n = _profile_args(profile_cycles)
         gdt, eadt, easqdt = self.codes
         with torch.cuda.device(self.device):
@@ -210,6 +212,10 @@ def _pack_entries(entries: Sequence[TensorState]):
     for e in entries:
         if e.p.device != dev or e.grad.device != dev:
             raise RuntimeError("multi_tensor_step: all tensors must be on one device")
+        for name, t in (("exp_avg", e.exp_avg), ("exp_avg_sq", e.exp_avg_sq), ("scale_m", e.scale_m),
+                        ("scale_v", e.scale_v), ("v_min", e.v_min)):
+            if t.device != dev and (t.numel() or name != "exp_avg_sq"):
+                raise RuntimeError(f"{name} must be on the params' device ({dev}), got {t.device}")
         if e.grad.dtype != gdt or e.exp_avg.dtype != eadt or e.exp_avg_sq.dtype != easqdt:
             raise RuntimeError("multi_tensor_step: grad and code dtypes must match across tensors")
         if e.p.dtype != torch.float32:
@@ -263,6 +269,8 @@ def multi_tensor_restore(entries: Sequence[TensorState], outs, block_size: int, 
     dst = storage_of(*outs[0])
     out = np.zeros(len(entries), dtype=STQ_CODE_OUT_DTYPE)
     dev = entries[0].p.device
+    if dev.type != "cuda":
+        raise RuntimeError("p/grad must be CUDA")
     for k, (e, (m, v)) in enumerate(zip(entries, outs)):
         if storage_of(e.exp_avg, e.exp_avg_sq) != src or storage_of(m, v) != dst:
             raise RuntimeError("multi_tensor_restore: one source and one destination storage per call")

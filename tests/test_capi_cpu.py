@@ -140,3 +140,29 @@ def test_restore_empty_list_is_a_no_op():
     L = mdq_hip.lib()
     assert L.stq_multi_tensor_mdq_adamw_restore(None, None, 0, 0, 2, 0, 128, 0, 0, None, 0, None) == _capi.STQ_OK
     assert call_restore(numel=0) == _capi.STQ_OK
+
+
+def _state(n=300, B=128, dev="cpu"):
+    nb = (n + B - 1) // B
+    import torch
+    return mdq_hip.TensorState(torch.zeros(n), torch.zeros(n), torch.full((n,), 8, dtype=torch.uint8),
+                               torch.empty(0, dtype=torch.uint8), torch.zeros(nb, device=dev),
+                               torch.zeros(nb), torch.full((nb,), -20.0), 1, 4, 1e-3, 0.9, 0.999, 1e-8, 0.01)
+
+
+def test_host_tensors_are_rejected_before_any_launch():
+    """The reference raises for non-CUDA tensors (stquant_kernel.cu:424-425); nothing reaches the
+    C ABI (which would hand host pointers to a kernel)."""
+    plan = mdq_hip.MultiTensorPlan([_state()], 128)
+    with pytest.raises(RuntimeError, match="p/grad must be CUDA"):
+        plan.run()
+    import torch
+    e = _state()
+    with pytest.raises(RuntimeError, match="p/grad must be CUDA"):
+        mdq_hip.multi_tensor_restore([e], [(torch.zeros(300, dtype=torch.int8), torch.zeros(300, dtype=torch.uint8))],
+                                     128)
+
+
+def test_state_tensors_on_another_device_are_rejected():
+    with pytest.raises(RuntimeError, match="scale_m must be on the params' device"):
+        mdq_hip.MultiTensorPlan([_state(dev="meta")], 128)
