@@ -140,3 +140,41 @@ def test_random_restore_matches_oracle(k):
         for name, t, a in zip(("scale_m", "scale_v", "v_min"), ts, hs):
             assert_bits_equal(f"tensor {i} {name}", t, a)
         assert_params_close(tp, hp_, p_prev)
+
+
+class WideCase(Case):
+    """Grads with magnitudes log-uniform over 1e-30 .. 1e3 (so v spans denormals to 1e6 and
+    x = v + 1e-12 straddles the fast v-code path's range), random signs, 10 % of quant blocks
+    all zero."""
+
+    def grads(self, rng):
+        g = (np.sign(rng.standard_normal(self.n)) * 10.0 ** rng.uniform(-30, 3, self.n)).astype(np.float32)
+        nb = (self.n + self.B - 1) // self.B
+        for b in np.nonzero(rng.random(nb) < 0.1)[0]:
+            g[b * self.B:(b + 1) * self.B] = 0.0
+        if self.grad_dtype == "bf16":
+            tg = torch.from_numpy(g).to(torch.bfloat16)
+            return tg.view(torch.int16).numpy().view(np.uint16).copy(), self._dev_view_t(tg)
+        return g, self._dev_view(g)
+
+
+WIDE = [(orc.STORE_P4, 4, 128, orc.ROUND_NEAREST), (orc.STORE_P4, 4, 64, orc.ROUND_STOCHASTIC),
+        (orc.STORE_S8, 8, 256, orc.ROUND_NEAREST), (orc.STORE_S8, 8, 128, orc.ROUND_STOCHASTIC),
+        (orc.STORE_S8, 3, 16, orc.ROUND_NEAREST), (orc.STORE_S16, 16, 128, orc.ROUND_NEAREST),
+        (orc.STORE_S16, 16, 1024, orc.ROUND_STOCHASTIC), (orc.STORE_S32, 32, 128, orc.ROUND_NEAREST),
+        (orc.STORE_S32, 24, 2, orc.ROUND_NEAREST)]
+
+
+@pytest.mark.parametrize("gdt", [np.float32, "bf16"])
+@pytest.mark.parametrize("storage,bits,B,rounding", WIDE)
+def test_extreme_gradient_magnitudes(storage, bits, B, rounding, gdt):
+    print(f"case: wide grads storage={storage} bits={bits} B={B} rounding={rounding} grad={gdt}", flush=True)
+    rng = np.random.default_rng(30_000 + 100 * storage + bits + B)
+    c = WideCase(B * 45 + 7, B, storage, rng, grad_dtype=gdt)
+    for step in range(1, 5):
+        g, tg = c.grads(rng)
+        p_prev = c.p.copy()
+        c.oracle_step(g, step, bits, rounding=rounding, seed=5, tensor_id=3)
+        mdq_hip.multi_tensor_step([c.entry(tg, step, bits, tensor_id=3)], B,
+                                  rounding="stochastic" if rounding else "nearest", seed=5)
+        c.check(p_prev)
