@@ -163,7 +163,7 @@ def build_workload(name, dev, seed=0, bits=None):
         o += n
         ob += nb
     plan = mdq_hip.MultiTensorPlan(entries, B)
-    return dict(plan=plan, N=N, tensors=len(sizes), B=B, bits=bits, gdt=gdt,
+    return dict(plan=plan, N=N, tensors=len(sizes), B=B, bits=bits, gdt=gdt, entries=entries,
                 grad_bytes=2 if gdt == "bf16" else 4, keep=(p, g, codes, vcodes, sm, sv, vm))
 
 
@@ -432,6 +432,10 @@ def main():
                     help="time storage-changing optimizer steps, device conversions vs torch passes")
     ap.add_argument("--bit-decision", action="store_true",
                     help="time the update-step bit decision, fused vs the reference's per-tensor path")
+    ap.add_argument("--shard-of", type=int, default=1,
+                    help="time one GPU's share of the set when it is sharded N ways at quant-block "
+                         "boundaries (each tensor cut into N block-aligned pieces; no communication)")
+    ap.add_argument("--shard-rank", type=int, default=0, help="which share --shard-of times")
     ap.add_argument("--copy-gib", type=float, default=0.0,
                     help="also run a plain device-to-device copy of this many GiB (rocprof calibration)")
     args = ap.parse_args()
@@ -462,6 +466,17 @@ def main():
         return
     w = build_workload(args.config, dev, bits=args.bits)
     plan = w["plan"]
+    shard = None
+    if args.shard_of > 1:
+        import mdq_hip
+        if not 0 <= args.shard_rank < args.shard_of:
+            sys.exit(f"bench.py: --shard-rank must be in [0, {args.shard_of})")
+        mine = mdq_hip.shard_states(w["entries"], w["B"], args.shard_of, args.shard_rank)
+        plan = mdq_hip.MultiTensorPlan(mine, w["B"])
+        shard = dict(of=args.shard_of, rank=args.shard_rank, tensors=len(mine),
+                     params=sum(e.p.numel() for e in mine))
+        w["N"] = shard["params"]
+        log(f"shard {args.shard_rank} of {args.shard_of}: {len(mine)} tensor pieces, {w['N']:,} params")
     torch.cuda.synchronize()
 
     step = 0
@@ -509,7 +524,7 @@ def main():
     # the factors that map a plain 4 GiB copy's counters to 4 GiB), committed under profiles/
     traffic, traffic_src = None, None
     prof_json = os.path.join(ROOT, "profiles", f"mdq_step_{args.config}_{w['gdt']}_{STORAGE_NAMES[w['bits']]}_b{w['B']}.json")
-    if os.path.exists(prof_json):
+    if os.path.exists(prof_json) and shard is None:
         with open(prof_json) as f:
             traffic = json.load(f)["traffic_bytes"]
         traffic_src = os.path.relpath(prof_json, ROOT)
@@ -521,8 +536,10 @@ def main():
         log(f"cpu baseline: {cpu['value']:.3e} params/s on {cpu['cores']} cores")
 
     out = {
-        "metric": METRICS.get(args.config, f"optimizer params updated/sec + achieved HBM GB/s (% peak), "
-                                           f"{args.config} set, 1 GPU"),
+        "metric": (METRICS.get(args.config, f"optimizer params updated/sec + achieved HBM GB/s (% peak), "
+                                            f"{args.config} set, 1 GPU") if shard is None else
+                   f"optimizer params updated/sec + achieved HBM GB/s (% peak), {args.config} set, "
+                   f"one GPU's share of {args.shard_of}"),
         "value": value,
         "unit": "params/s",
         "n_gpus": 1,
@@ -535,7 +552,10 @@ def main():
         "dtype": "f32",
         "data": "synthetic",
         "config": {
-            "workload": f"{args.config}: {w['tensors']} tensors, {N} fp32 params, {w['gdt']} grads, "
+            "workload": (f"{args.config}: {w['tensors']} tensors, " if shard is None else
+                         f"{args.config} share {args.shard_rank} of {args.shard_of} (block-aligned pieces of "
+                         f"{shard['tensors']} tensors): ") +
+                        f"{N} fp32 params, {w['gdt']} grads, "
                         f"{w['bits']}-bit {'packed ' if w['bits'] == 4 else ''}m/v codes, block {w['B']}, "
                         f"nearest rounding, one multi-tensor launch",
             "params": N,

@@ -237,6 +237,41 @@ def _pack_entries(entries: Sequence[TensorState]):
     return arr, (dtype_code(gdt), dtype_code(eadt), dtype_code(easqdt))
 
 
+def block_aligned_ranges(numel: int, block_size: int, world: int):
+    """``[(start, end)] * world``: one tensor's elements cut into ``world`` contiguous pieces at
+    quant-block boundaries of B = min(block_size, 1024), balanced by whole blocks (the first
+    ``nblocks % world`` pieces hold one block more; the last non-empty piece ends at ``numel``).
+    Blocks are independent, so stepping every piece gives exactly the whole tensor's step."""
+    if world < 1:
+        raise ValueError("world must be >= 1")
+    B = min(int(block_size), 1024)
+    nb = (numel + B - 1) // B
+    q, r = divmod(nb, world)
+    out, b = [], 0
+    for k in range(world):
+        nk = q + (1 if k < r else 0)
+        out.append((min(b * B, numel), min((b + nk) * B, numel)))
+        b += nk
+    return out
+
+
+def shard_states(entries: Sequence[TensorState], block_size: int, world: int, rank: int):
+    """The TensorState views of piece ``rank`` of every tensor (block_aligned_ranges); tensors
+    whose piece is empty are left out."""
+    B = min(int(block_size), 1024)
+    out = []
+    for e in entries:
+        s, t = block_aligned_ranges(e.p.numel(), block_size, world)[rank]
+        if s == t:
+            continue
+        b0, b1 = s // B, (t + B - 1) // B
+        vsq = e.exp_avg_sq if e.exp_avg_sq.numel() == 0 else e.exp_avg_sq.view(-1)[s:t]
+        out.append(TensorState(e.p.view(-1)[s:t], e.grad.view(-1)[s:t], e.exp_avg.view(-1)[s:t], vsq,
+                               e.scale_m[b0:b1], e.scale_v[b0:b1], e.v_min[b0:b1], e.step, e.bits, e.lr,
+                               e.beta1, e.beta2, e.eps, e.weight_decay, e.tensor_id))
+    return out
+
+
 def multi_tensor_step(entries: Sequence[TensorState], block_size: int, *,
                       rounding=ROUND_NEAREST, seed: int = 0,
                       profile_cycles: Optional[torch.Tensor] = None) -> None:
