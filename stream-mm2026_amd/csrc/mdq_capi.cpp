@@ -93,6 +93,16 @@ int storage_width(int st)
 
 int code_bytes(int st) { return st == mdq::ST_P4 ? 1 : storage_width(st) / 8; }
 
+const char *storage_name(int st)
+{
+    switch (st) {
+    case mdq::ST_P4: return "packed nibbles";
+    case mdq::ST_S8: return "int8/uint8";
+    case mdq::ST_S16: return "int16/uint16";
+    default: return "int32/uint32";
+    }
+}
+
 
 bool is_aligned(const void *ptr, int bytes) { return ((uintptr_t)ptr % (uintptr_t)bytes) == 0; }
 
@@ -477,7 +487,8 @@ int run_restore(const stq_tensor *tensors, const stq_code_out *out, int n_tensor
         const stq_code_out &o = out[i];
         const std::string at = "tensor " + std::to_string(i) + ": ";
         if (final_storage(t.bits) != dst && !(dst == mdq::ST_S8 && t.bits == 4))
-            return fail(STQ_ERR_INVALID, "%sbits=%d is not stored in destination storage %d", at.c_str(), t.bits, dst);
+            return fail(STQ_ERR_INVALID, "%sbits=%d is not stored in destination storage %d (%s)", at.c_str(), t.bits,
+                        dst, storage_name(dst));
         if (t.numel < 0) return fail(STQ_ERR_INVALID, "%snumel must be >= 0", at.c_str());
         if (src == mdq::ST_P4 ? t.exp_avg_numel != t.numel
                               : (t.exp_avg_numel < t.numel || t.exp_avg_sq_numel < t.numel))
