@@ -137,7 +137,7 @@ int stq_multi_tensor_mdq_adamw(const stq_tensor *tensors, int n_tensors,
  * 1e-12 add are fp32, as the reference's.  Differs from the reference's fp32
  * torch reductions by rounding only (about 1e-7 relative).  grads and numels
  * are host arrays; the library keeps the descriptor table and the partial
- * sums (24 bytes per 16384 elements) in its per-device ring.
+ * sums (24 bytes per 32768 elements) in its per-device ring.
  *
  * Replaces MDQAdamWSimple._compute_grad_stats called once per tensor
  * (/root/reference/CUDA/stquant_opt_simple.py:93-98, loop at :427-431).

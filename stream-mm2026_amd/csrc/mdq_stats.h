@@ -6,8 +6,8 @@
 
 namespace mdq {
 
-// Elements per workgroup tile of the partial-sum kernel (256 threads x 64).
-constexpr int STAT_TILE = 16384;
+// Elements per workgroup tile of the partial-sum kernel (512 threads x 64).
+constexpr int STAT_TILE = 32768;
 
 // One tensor of a statistics launch: tiles [tile_begin, tile_end) of the
 // launch cover its numel elements (none when numel == 0).

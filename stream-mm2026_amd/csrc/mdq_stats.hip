@@ -4,7 +4,7 @@
 // The reference computes, per tensor and before the step (stquant_opt_simple.py:93-98),
 //   n_l = sqrt(mean(g^2)),  r_l = std(g) / (mean(|g|) + 1e-12),  v_l = mean(g^2)
 // with std unbiased, as separate torch reductions per tensor.  Here:
-//   1. stats_partial_kernel: one workgroup per 16384-element tile of one tensor
+//   1. stats_partial_kernel: one 512-thread workgroup per 32768-element tile of one tensor
 //      accumulates sum g, sum g^2, sum |g| in fp64 (each fp32 square is exact
 //      in fp64) and writes the three partial sums of its tile;
 //   2. stats_finish_kernel: one workgroup per tensor adds its tiles' partials
@@ -19,7 +19,7 @@ namespace mdq {
 
 namespace {
 
-constexpr int ST_THREADS = 256;
+constexpr int ST_THREADS = 512;
 constexpr int ST_WAVES = ST_THREADS / 64;
 
 __device__ __forceinline__ float bf16_to_f(uint32_t h) { return __uint_as_float(h << 16); }

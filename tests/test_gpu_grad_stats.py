@@ -1,7 +1,7 @@
 """Fused multi-tensor gradient statistics and the vectorised bit decision on the GPU.
 
 - ``mdq_hip.grad_stats`` against the oracle (float64 sums, tests/test_oracle_grad_stats.py)
-  within 1e-6 relative, over ragged sizes (tile edges at 16384), fp32/bf16/fp16 and
+  within 1e-6 relative, over ragged sizes (tile edges at 16384 and 32768), fp32/bf16/fp16 and
   unaligned views; NaN where torch gives NaN (numel 0 and 1);
 - deterministic (bit-identical on repeat), and within 1e-5 of the reference's fp32 torch
   reductions run on the same device;
@@ -19,7 +19,7 @@ from stquant_opt_simple import MDQAdamWSimple
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
-SIZES = [1, 2, 3, 0, 16383, 16384, 16385, 49153, 100_003, (1 << 20) + 7, 64]
+SIZES = [1, 2, 3, 0, 16383, 16384, 16385, 32767, 32768, 32769, 49153, 100_003, (1 << 20) + 7, 64]
 
 
 def views(dtype, offset, seed):
