@@ -1,14 +1,20 @@
 // mdq_kernel.h -- the fused dequant -> AdamW -> requant step for gfx950.
 //
-// One launch walks every tensor of a (storage, grad dtype, block size,
-// rounding) class from a packed MdqDesc table.  Semantics per element follow
-// /root/reference/CUDA/stquant_kernel.cu:53-401 (see mdq_step_tile below for
-// the line-by-line map); the layout and schedule are this file's own:
+// One launch walks every tensor of a (code storage, grad dtype, block size,
+// rounding) class from a packed MdqDesc table.  The codes are read in a source
+// storage and written in a destination storage: the same for an ordinary
+// step, different for a step whose bit width changed (the reference's align ->
+// kernel -> pack, /root/reference/CUDA/stquant_opt_simple.py:140-280, in one
+// pass).  Semantics per element follow /root/reference/CUDA/stquant_kernel.cu:
+// 53-401 (see mdq_step_tile below for the line-by-line map); the layout and
+// schedule are this file's own:
 //
-// * A tile is 256 lanes x EPL elements (EPL = 8 for B >= 8).  A quant block
-//   of B elements is owned by LPB = B/EPL consecutive lanes of one wave (two
-//   waves for B = 1024); lane j of a block owns quads j, j+LPB, ... so every
-//   16-lane row of a wave reads one contiguous 256-byte span per 16-byte load.
+// * A tile is one wave x EPL elements (EPL = 8 for B >= 8; two waves for
+//   B = 1024), one workgroup per tile.  A quant block of B elements is owned by
+//   LPB = B/EPL consecutive lanes; lane j of a block owns quads j, j+LPB, ...,
+//   so every 16-lane row reads one contiguous 256-byte span per 16-byte load,
+//   or, when 1-byte codes are involved and LPB is 8, 16 or 32, the permuted
+//   quads of paired_codes below (8-byte code accesses plus one lane swap).
 // * Block reductions (max|m|, max/min log v) run in registers, then across
 //   the LPB lanes with DPP row operations (quad_perm, row_half_mirror,
 //   row_mirror), ds_swizzle for 32 lanes, ds_bpermute for 64, and an LDS
