@@ -1,6 +1,8 @@
 // mdq_dispatch.h -- run-time (grad dtype, block size, rounding) -> template
-// instance dispatch for one storage class.  Included once per storage by
-// mdq_kernels_<storage>.hip so the four classes compile in parallel.
+// instance dispatch.  Included by mdq_kernels_<storage>.hip (steps that keep
+// their storage, every block size) and mdq_kernels_tr_<storage>.hip (steps
+// into that storage from another one, block sizes 64 / 128 / 256), so the
+// instance sets compile in parallel.
 #pragma once
 #include "mdq_kernel.h"
 #include "mdq_launch.h"
