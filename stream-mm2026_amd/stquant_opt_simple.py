@@ -7,11 +7,14 @@ block, ``current_bit``, ``last_score``), ``state_dict`` extras, bit-distribution
 getters and timing keys as the reference.
 
 What differs is underneath: instead of one kernel launch per tensor bracketed by
-two device synchronisations (:242-265), ``step()`` aligns the code storage of
-every tensor exactly as the reference does (:140-210), then runs ONE
-multi-tensor HIP launch per storage class through the C ABI of
-``libstquant_hip.so`` (``mdq_hip.multi_tensor_step``).  Results per element are
-those of the reference kernel (:246-263 -> stquant_kernel.cu).
+two device synchronisations (:242-265), ``step()`` runs ONE multi-tensor HIP
+launch per storage class through the C ABI of ``libstquant_hip.so``
+(``mdq_hip.multi_tensor_step``).  Tensors whose bit width changed go through
+one launch of the storage-changing step (``mdq_hip.multi_tensor_restore``: the
+reference's align -> kernel -> pack of :140-280 in one pass, block sizes
+64 / 128 / 256), or else through device conversions with exactly the
+reference's storage rules (:140-210).  Results per element are those of the
+reference kernel (:246-263 -> stquant_kernel.cu).
 
 New optional param-group keys (defaults keep the reference behaviour):
 ``bits`` (fixed code width 4/8/16/32 instead of the score-based choice),
