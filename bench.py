@@ -170,7 +170,7 @@ def build_workload(name, dev, seed=0, bits=None):
 ALIGN_ELEMS = 256
 
 
-def sweep_config5(dev, steps: int, warmup: int):
+def sweep_config5(dev, steps: int, warmup: int, packed_views: bool = False):
     """Config 5 over {4, 8}-bit x B {64, 128, 256} x {nearest, stochastic}: ms/step, GB/s, params/s."""
     import torch
 
@@ -181,14 +181,21 @@ def sweep_config5(dev, steps: int, warmup: int):
     gen = torch.Generator(device=dev).manual_seed(5)
     points = []
     for B in (64, 128, 256):
-        # each tensor starts on a 1 KiB boundary of p, as separate torch allocations would
+        # each tensor starts on a 1 KiB boundary, as separate torch allocations would; with
+        # packed_views the params and grads are views of one buffer packed back to back (odd
+        # element offsets) while the codes and scales stay separate, as the optimizer allocates them
         offs = [0]
         for n in sizes:
             offs.append(offs[-1] + (n + ALIGN_ELEMS - 1) // ALIGN_ELEMS * ALIGN_ELEMS)
         NP = offs[-1]
+        offs_pg = [0]
+        for n in sizes:
+            offs_pg.append(offs_pg[-1] + n)
+        if not packed_views:
+            offs_pg = offs
         p = torch.empty(NP, dtype=torch.float32, device=dev).normal_(0.0, 0.02, generator=gen)
         g = torch.zeros(NP, dtype=torch.float32, device=dev)
-        for n, o in zip(sizes, offs):
+        for n, o in zip(sizes, offs_pg):
             g[o:o + n] = config5_grads_device(n, B, gen, dev)
         nbs = [(n + B - 1) // B for n in sizes]
         NB = sum(nbs)
@@ -203,9 +210,9 @@ def sweep_config5(dev, steps: int, warmup: int):
             sv = torch.zeros(NB, device=dev)
             vm = torch.full((NB,), -20.0, device=dev)
             entries, ob = [], 0
-            for i, (n, nb, o) in enumerate(zip(sizes, nbs, offs)):
+            for i, (n, nb, o, opg) in enumerate(zip(sizes, nbs, offs, offs_pg)):
                 entries.append(mdq_hip.TensorState(
-                    p[o:o + n], g[o:o + n], cm[o:o + n], cv if bits == 4 else cv[o:o + n],
+                    p[opg:opg + n], g[opg:opg + n], cm[o:o + n], cv if bits == 4 else cv[o:o + n],
                     sm[ob:ob + nb], sv[ob:ob + nb], vm[ob:ob + nb], 1, bits, 1e-3, 0.9, 0.999, 1e-8, 0.01, i))
                 ob += nb
             for rounding in ("nearest", "stochastic"):
@@ -235,7 +242,7 @@ def sweep_config5(dev, steps: int, warmup: int):
             del cm, cv, sm, sv, vm, entries, plan
         del p, g
         torch.cuda.empty_cache()
-    return dict(params=N, tensors=len(sizes), points=points)
+    return dict(params=N, tensors=len(sizes), packed_views=packed_views, points=points)
 
 
 def e2e_gpt2(steps: int, warmup: int, out_path):
@@ -424,6 +431,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--sweep-config5", action="store_true",
                     help="time BASELINE config 5 over bits x block x rounding (one JSON line with all points)")
+    ap.add_argument("--packed-views", action="store_true",
+                    help="with --sweep-config5: params and grads as views packed back to back (odd offsets)")
     ap.add_argument("--e2e-gpt2", action="store_true",
                     help="BASELINE config 3: GPT-2 small pretraining, stochastic vs nearest vs AdamW")
     ap.add_argument("--e2e-steps", type=int, default=300)
@@ -449,7 +458,7 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     if args.sweep_config5:
-        res = sweep_config5(dev, args.steps, args.warmup)
+        res = sweep_config5(dev, args.steps, args.warmup, packed_views=args.packed_views)
         print(json.dumps({"metric": "config 5 sweep: params/s and HBM GB/s per point", "n_gpus": 1,
                           "steps": args.steps, "warmup": args.warmup, "data": "synthetic", **res}), flush=True)
         return

@@ -163,9 +163,10 @@ int make_desc(const stq_tensor &t, int storage, int grad_dt, int B, MdqDesc &d)
     const int cb = code_bytes(storage);
     // full tiles move codes in 4-element quads (4 * cb bytes), 1-byte codes in 8-byte pairs
     const int ca = (storage == mdq::ST_S8 || storage == mdq::ST_P4) ? 8 : 4 * cb;
-    bool al = is_aligned(t.p, 16) && is_aligned(t.grad, 4 * gb) && is_aligned(t.exp_avg, ca) &&
-              (storage == mdq::ST_P4 || is_aligned(t.exp_avg_sq, ca));
-    d.flags = al ? mdq::DF_ALIGNED : 0u;
+    const bool codes_al = is_aligned(t.exp_avg, ca) && (storage == mdq::ST_P4 || is_aligned(t.exp_avg_sq, ca));
+    const bool pg_al = is_aligned(t.p, 16) && is_aligned(t.grad, 4 * gb);
+    // p and grads are always element-aligned (fp32 p, 2- or 4-byte grads): element accesses need no more
+    d.flags = (codes_al ? mdq::DF_CODES_ALIGNED : 0u) | (codes_al && pg_al ? mdq::DF_ALIGNED : 0u);
     return STQ_OK;
 }
 
@@ -519,7 +520,7 @@ int run_restore(const stq_tensor *tensors, const stq_code_out *out, int n_tensor
         d.code_m = t.exp_avg;
         d.code_v = src == mdq::ST_P4 ? nullptr : t.exp_avg_sq;
         if (!(is_aligned(d.code_m, sca) && (src == mdq::ST_P4 || is_aligned(d.code_v, sca))))
-            d.flags &= ~mdq::DF_ALIGNED;
+            d.flags &= ~(mdq::DF_ALIGNED | mdq::DF_CODES_ALIGNED);
         d.tile_begin = tiles;
         tiles += (t.numel + te - 1) / te;
         d.tile_end = tiles;

@@ -13,7 +13,8 @@ enum Storage : int { ST_P4 = 0, ST_S8 = 1, ST_S16 = 2, ST_S32 = 3 };
 enum GradType : int { GT_F32 = 0, GT_BF16 = 1, GT_F16 = 2 };
 
 enum DescFlags : uint32_t {
-    DF_ALIGNED = 1u,  // every pointer meets the 16-byte vector-access alignment
+    DF_ALIGNED = 1u,        // every pointer meets the vector-access alignment
+    DF_CODES_ALIGNED = 2u,  // the code pointers do (p and grads may not)
 };
 
 struct alignas(16) MdqDesc {

@@ -149,6 +149,9 @@ template <> struct GradIO<GT_F32> {
     static __device__ __forceinline__ float load1(const void *g, int64_t i) {
         return ld_g<float>(static_cast<const float *>(g) + i);
     }
+    static __device__ __forceinline__ float load1nt(const void *g, uint32_t i) {
+        return ld_nt<float>(static_cast<const float *>(g) + i);
+    }
 };
 template <> struct GradIO<GT_BF16> {
     static __device__ __forceinline__ void load4(const void *g, int64_t i, float *o) {
@@ -158,6 +161,9 @@ template <> struct GradIO<GT_BF16> {
     }
     static __device__ __forceinline__ float load1(const void *g, int64_t i) {
         return bits_f((uint32_t)ld_g<uint16_t>(static_cast<const uint16_t *>(g) + i) << 16);
+    }
+    static __device__ __forceinline__ float load1nt(const void *g, uint32_t i) {
+        return bits_f((uint32_t)ld_nt<uint16_t>(static_cast<const uint16_t *>(g) + i) << 16);
     }
 };
 template <> struct GradIO<GT_F16> {
@@ -171,6 +177,9 @@ template <> struct GradIO<GT_F16> {
     }
     static __device__ __forceinline__ float load1(const void *g, int64_t i) {
         return h2f(ld_g<uint16_t>(static_cast<const uint16_t *>(g) + i));
+    }
+    static __device__ __forceinline__ float load1nt(const void *g, uint32_t i) {
+        return h2f(ld_nt<uint16_t>(static_cast<const uint16_t *>(g) + i));
     }
 };
 
@@ -457,10 +466,15 @@ __device__ __forceinline__ float dequant_m(float code, float sm, float neg8sm)
 }
 
 // ---------------------------------------------------------------- one tile
-// FULL: every element of the tile lies inside the tensor and all pointers are
-// 16-byte aligned, so vector accesses are used; otherwise every access is
-// guarded by idx < numel.
-template <int SRC, int DST, int GT, int LOG2B, bool SR, bool FULL>
+// Tile modes.  TILE_VECTOR: every element of the tile lies inside the tensor and
+// all pointers are 16-byte aligned, so vector accesses are used.  TILE_ELEM_PG:
+// the tile lies inside the tensor and the codes are aligned, but p or the grads
+// are not (views at odd element offsets of one buffer): codes move as in
+// TILE_VECTOR, p and grads one element per access, with no bounds guards.
+// TILE_GUARDED: every access element by element, guarded by idx < numel.
+enum TileMode : int { TILE_GUARDED = 0, TILE_VECTOR = 1, TILE_ELEM_PG = 2 };
+
+template <int SRC, int DST, int GT, int LOG2B, bool SR, int MODE>
 __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int lane, int wave,
                                               float *lut, int32_t *xw, unsigned long long seed,
                                               bool prof_on, ProfAcc &pa)
@@ -469,6 +483,9 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
     constexpr int B = C::B, EPL = C::EPL, LPB = C::LPB;
     constexpr bool USE_LUT = (SRC == ST_P4) && B >= 32;
     constexpr bool PAIRED = paired_codes<SRC, DST, LOG2B>();
+    constexpr bool FULL = MODE != TILE_GUARDED;           // the whole tile lies inside the tensor
+    constexpr bool VEC_PG = MODE == TILE_VECTOR;          // p and grads move as 16-byte vectors
+    static_assert(MODE != TILE_ELEM_PG || C::QPL > 0, "element p/g mode needs 4-element quads");
 
     unsigned long long t0 = 0;
     if (prof_on) t0 = clock64();
@@ -509,9 +526,17 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
 #pragma unroll
         for (int k = 0; k < C::QPL; ++k) {
             const uint32_t i = lbase + 4 * lane_quad<PAIRED, LOG2B>(j, k);
-            vf4 p4 = ld_nt<vf4>(dt.p + i);
-            pv[4 * k + 0] = p4.x; pv[4 * k + 1] = p4.y; pv[4 * k + 2] = p4.z; pv[4 * k + 3] = p4.w;
-            GradIO<GT>::load4(dt.g, i, gv + 4 * k);
+            if constexpr (VEC_PG) {
+                vf4 p4 = ld_nt<vf4>(dt.p + i);
+                pv[4 * k + 0] = p4.x; pv[4 * k + 1] = p4.y; pv[4 * k + 2] = p4.z; pv[4 * k + 3] = p4.w;
+                GradIO<GT>::load4(dt.g, i, gv + 4 * k);
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    pv[4 * k + c] = ld_nt<float>(dt.p + i + c);
+                    gv[4 * k + c] = GradIO<GT>::load1nt(dt.g, i + c);
+                }
+            }
             if constexpr (!(PAIRED && one_byte_codes(SRC))) CodeIO<SRC>::load4(dt, i, mc + 4 * k, vc + 4 * k);
         }
         if constexpr (PAIRED && one_byte_codes(SRC)) CodeIO<SRC>::template load8<LPB / 2>(dt, lbase, j, mc, vc);
@@ -844,8 +869,13 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
                 if constexpr (DST == ST_P4) CodeIO<DST>::store4f(ot, i, pk + 4 * k);
                 else CodeIO<DST>::store4(ot, i, qmi + 4 * k, qvi + 4 * k);
             }
-            vf4 o = {pv[4 * k + 0], pv[4 * k + 1], pv[4 * k + 2], pv[4 * k + 3]};
-            st_nt<vf4>(o, dt.p + i);
+            if constexpr (VEC_PG) {
+                vf4 o = {pv[4 * k + 0], pv[4 * k + 1], pv[4 * k + 2], pv[4 * k + 3]};
+                st_nt<vf4>(o, dt.p + i);
+            } else {
+#pragma unroll
+                for (int c = 0; c < 4; ++c) st_nt<float>(pv[4 * k + c], dt.p + i + c);
+            }
         }
         if constexpr (PAIRED && one_byte_codes(DST)) {
             if constexpr (DST == ST_P4) CodeIO<DST>::template store8f<LPB / 2>(ot, lbase, j, pk);
@@ -900,9 +930,15 @@ __global__ __launch_bounds__(Cfg<LOG2B>::THREADS) void mdq_step_kernel(const Mdq
     const long long tl = tile - d.tile_begin;
     const bool prof_on = prof != nullptr && (tile & 63) == 0;
     ProfAcc pa = {{0, 0, 0, 0, 0}};
-    const bool full = (d.flags & DF_ALIGNED) && (tl + 1) * C::TILE <= d.numel;
-    if (full) mdq_step_tile<SRC, DST, GT, LOG2B, SR, true>(d, tl, lane, wave, lut_s, xw_s, seed, prof_on, pa);
-    else mdq_step_tile<SRC, DST, GT, LOG2B, SR, false>(d, tl, lane, wave, lut_s, xw_s, seed, prof_on, pa);
+    const bool inside = (tl + 1) * C::TILE <= d.numel;
+    if (inside && (d.flags & DF_ALIGNED)) {
+        mdq_step_tile<SRC, DST, GT, LOG2B, SR, TILE_VECTOR>(d, tl, lane, wave, lut_s, xw_s, seed, prof_on, pa);
+    } else if (C::QPL > 0 && inside && (d.flags & DF_CODES_ALIGNED)) {
+        if constexpr (C::QPL > 0)
+            mdq_step_tile<SRC, DST, GT, LOG2B, SR, TILE_ELEM_PG>(d, tl, lane, wave, lut_s, xw_s, seed, prof_on, pa);
+    } else {
+        mdq_step_tile<SRC, DST, GT, LOG2B, SR, TILE_GUARDED>(d, tl, lane, wave, lut_s, xw_s, seed, prof_on, pa);
+    }
     if (prof_on && threadIdx.x == 0) {
 #pragma unroll
         for (int s = 0; s < 5; ++s) atomicAdd(prof + s, pa.c[s]);

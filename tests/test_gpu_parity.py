@@ -60,16 +60,18 @@ def resync_params(tp, p):
 class Case:
     """One tensor's numpy state (oracle side) and torch state (device side)."""
 
-    def __init__(self, n, B, storage, rng, grad_dtype=np.float32, offset=0):
+    def __init__(self, n, B, storage, rng, grad_dtype=np.float32, offset=0, codes_aligned=False):
         self.n, self.B, self.storage = n, B, storage
         self.p = (rng.standard_normal(n) * 0.02).astype(np.float32)
         self.state = list(orc.init_state(n, B, storage))
         self.offset = offset
-        # device copies; `offset` elements of padding in front make the views unaligned
+        # device copies; `offset` elements of padding in front make the views unaligned (the code
+        # arrays too unless `codes_aligned`, as when only params and grads are views of one buffer)
         self.tp = self._dev_view(self.p)
         cm, cv = self.state[0], self.state[1]
-        self.tcm = self._dev_view(cm)
-        self.tcv = self._dev_view(cv) if cv is not None else torch.empty(0, dtype=torch.uint8, device=DEV)
+        cview = (lambda a: to_dev(a.copy())) if codes_aligned else self._dev_view
+        self.tcm = cview(cm)
+        self.tcv = cview(cv) if cv is not None else torch.empty(0, dtype=torch.uint8, device=DEV)
         self.tsm, self.tsv, self.tvm = (to_dev(a.copy()) for a in self.state[2:])
         self.grad_dtype = grad_dtype
 
@@ -230,6 +232,24 @@ def test_unaligned_views_take_the_guarded_path():
         p_prev = c.p.copy()
         c.oracle_step(g, step, 8)
         mdq_hip.multi_tensor_step([c.entry(tg, step, 8)], 128)
+        c.check(p_prev)
+
+
+@pytest.mark.parametrize("storage,bits", STORAGE_BITS)
+@pytest.mark.parametrize("B,offset,gdt", [(128, 1, np.float32), (64, 3, "bf16"), (256, 2, np.float16),
+                                          (1024, 1, "bf16"), (4, 5, np.float32)])
+def test_param_and_grad_views_at_odd_offsets(storage, bits, B, offset, gdt):
+    """Params and grads as views at odd element offsets of one buffer, codes allocated on their own
+    (the optimizer's layout when a model's params are views of a flat buffer): whole tiles take the
+    element-wise p / grad accesses with vector code accesses, the tail tile the guarded path."""
+    print(f"case: p/g views offset={offset} storage={storage} bits={bits} B={B} grad={gdt}", flush=True)
+    rng = np.random.default_rng(40_000 + 10 * offset + B + storage)
+    c = Case(B * 29 + 3 * B // 4 + 1, B, storage, rng, grad_dtype=gdt, offset=offset, codes_aligned=True)
+    for step in (1, 2):
+        g, tg = c.grads(rng)
+        p_prev = c.p.copy()
+        c.oracle_step(g, step, bits)
+        mdq_hip.multi_tensor_step([c.entry(tg, step, bits)], B)
         c.check(p_prev)
 
 
