@@ -18,10 +18,12 @@ from . import _capi
 from ._capi import ROUND_NEAREST, ROUND_STOCHASTIC, StqTensor, check, dtype_code, lib
 
 __all__ = [
-    "ROUND_NEAREST", "ROUND_STOCHASTIC", "TensorState", "MultiTensorPlan", "fused_step",
-    "multi_tensor_step",
-    "device_math", "device_math_digests", "host_math", "host_round_half_away", "host_div_code_range",
-    "host_philox",
+    "ROUND_NEAREST", "ROUND_STOCHASTIC", "STORE_P4", "STORE_S8", "STORE_S16", "STORE_S32",
+    "TensorState", "MultiTensorPlan", "fused_step", "multi_tensor_step", "multi_tensor_restore",
+    "RESTORE_BLOCK_SIZES", "grad_stats", "convert_codes", "empty_codes", "storage_of",
+    "block_aligned_ranges", "shard_states",
+    "device_math", "device_math_digests", "device_log_approx_error", "host_math", "host_round_half_away",
+    "host_div_code_range", "host_philox",
     "lib", "rounding_code",
 ]
 
@@ -75,6 +77,10 @@ def fused_step(p, grad, exp_avg, exp_avg_sq, scale_m, scale_v, v_min,
         _check_dense(name, t)
     for name, t in (("p", p), ("grad", grad), ("exp_avg", exp_avg), ("exp_avg_sq", exp_avg_sq)):
         _check_dense(name, t)
+    for name, t in (("grad", grad), ("exp_avg", exp_avg), ("exp_avg_sq", exp_avg_sq), ("scale_m", scale_m),
+                    ("scale_v", scale_v), ("v_min", v_min)):
+        if t.device != p.device and (t.numel() or name != "exp_avg_sq"):
+            raise RuntimeError(f"{name} must be on the params' device ({p.device}), got {t.device}")
     if exp_avg_sq.numel() and not exp_avg_sq.is_cuda:
         raise RuntimeError("exp_avg_sq must be CUDA")
     prof_ptr, prof_n = _profile_args(profile_cycles)
@@ -442,8 +448,7 @@ def device_math_digests(which: str, first: int, count: int, chunk: int, device=N
     return dig
 
 
-def host_math(which: str, x) -> "numpy.ndarray":  # noqa: F821
-    import numpy as np
+def host_math(which: str, x) -> np.ndarray:
     x = np.ascontiguousarray(x, dtype=np.float32)
     y = np.empty_like(x)
     lib().stq_host_math(0 if which == "exp" else 1, x.ctypes.data, y.ctypes.data, x.size)
@@ -451,7 +456,6 @@ def host_math(which: str, x) -> "numpy.ndarray":  # noqa: F821
 
 
 def host_round_half_away(u, d, inv_ulps: int = 0):
-    import numpy as np
     u = np.ascontiguousarray(u, dtype=np.float32)
     d = np.ascontiguousarray(d, dtype=np.float32)
     out = np.empty_like(u)
@@ -460,7 +464,6 @@ def host_round_half_away(u, d, inv_ulps: int = 0):
 
 
 def host_div_code_range(x, bits: int):
-    import numpy as np
     x = np.ascontiguousarray(x, dtype=np.float32)
     out = np.empty_like(x)
     lib().stq_host_div_code_range(x.ctypes.data, out.ctypes.data, x.size, int(bits))
@@ -468,7 +471,6 @@ def host_div_code_range(x, bits: int):
 
 
 def host_philox(ctr, key):
-    import numpy as np
     c = np.ascontiguousarray(np.asarray(ctr, dtype=np.uint32).reshape(4))
     k = np.ascontiguousarray(np.asarray(key, dtype=np.uint32).reshape(2))
     out = np.zeros(4, dtype=np.uint32)
