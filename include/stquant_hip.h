@@ -85,7 +85,14 @@ int stq_fused_mdq_adamw(float *p, const void *grad, int grad_dtype, int64_t grad
                         int rounding, uint64_t seed, uint32_t tensor_id,
                         void *stream);
 
-/* One tensor of a multi-tensor step; fields as in stq_fused_mdq_adamw. */
+/*
+ * One tensor of a multi-tensor step; fields as in stq_fused_mdq_adamw, plus
+ * elem_offset: the index of element 0 in the stochastic-rounding stream of
+ * tensor_id (0 for a whole tensor; for a piece of a larger tensor, the piece's
+ * start within it, so that stepping every piece draws the same random numbers
+ * as stepping the whole tensor).  It must be >= 0 and a multiple of
+ * min(block_size, 1024); nearest rounding does not use it.
+ */
 typedef struct stq_tensor {
     float *p;
     const void *grad;
@@ -105,6 +112,7 @@ typedef struct stq_tensor {
     int32_t step;
     int32_t bits;
     uint32_t tensor_id;
+    int64_t elem_offset;
 } stq_tensor;
 
 /*

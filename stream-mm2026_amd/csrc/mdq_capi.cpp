@@ -124,6 +124,9 @@ int make_desc(const stq_tensor &t, int storage, int grad_dt, int B, MdqDesc &d)
                     (long long)t.numel);
     }
     if (t.step < 1) return fail(STQ_ERR_INVALID, "step must be >= 1 (incremented by the caller), got %d", t.step);
+    if (t.elem_offset < 0 || t.elem_offset % B != 0)
+        return fail(STQ_ERR_INVALID, "elem_offset (%lld) must be >= 0 and a multiple of the block size %d",
+                    (long long)t.elem_offset, B);
     const int64_t nb = (t.numel + B - 1) / B;
     if (t.scale_m_numel < nb || t.scale_v_numel < nb || t.v_min_numel < nb)
         return fail(STQ_ERR_INVALID, "scale_m / scale_v / v_min need ceil(numel / %d) = %lld elements", B,
@@ -159,6 +162,7 @@ int make_desc(const stq_tensor &t, int storage, int grad_dt, int B, MdqDesc &d)
     d.bits = (uint32_t)t.bits;
     d.step = (uint32_t)t.step;
     d.tensor_id = t.tensor_id;
+    d.rng_origin = t.elem_offset;
     const int gb = grad_dt == STQ_FLOAT ? 4 : 2;
     const int cb = code_bytes(storage);
     // full tiles move codes in 4-element quads (4 * cb bytes), 1-byte codes in 8-byte pairs
@@ -626,6 +630,7 @@ int stq_fused_mdq_adamw(float *p, const void *grad, int grad_dtype, int64_t grad
     t.step = step;
     t.bits = bits;
     t.tensor_id = tensor_id;
+    t.elem_offset = 0;
     return run(&t, 1, grad_dtype, exp_avg_dtype, exp_avg_sq_dtype, block_size, rounding, seed,
                profile_cycles, profile_numel, stream);
 }

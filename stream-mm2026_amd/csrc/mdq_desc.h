@@ -45,6 +45,9 @@ struct alignas(16) MdqDesc {
     // code_m / code_v); unused when the storage stays.
     void *out_m;
     void *out_v;
+    // Index of element 0 in the tensor's stochastic-rounding stream (a
+    // multiple of B; nonzero for a piece of a larger tensor).
+    int64_t rng_origin;
 };
 
 static_assert(sizeof(MdqDesc) % 16 == 0, "descriptor must stay 16-byte sized");

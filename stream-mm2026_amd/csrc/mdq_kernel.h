@@ -712,10 +712,12 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
             // Philox4x32-10 per 4-element quad of the tensor: counter
             // (quad index lo, hi, tensor id, step), key = seed; word i of the
             // output serves element 4q+i (low half -> m, high half -> v).
+            // Element indices count from rng_origin (a multiple of B, so of 4
+            // wherever a lane owns whole quads).
             if constexpr (C::QPL > 0) {
 #pragma unroll
                 for (int k = 0; k < C::QPL; ++k) {
-                    const uint64_t q = (uint64_t)((base >> 2) + lane_quad<PAIRED, LOG2B>(j, k));
+                    const uint64_t q = (uint64_t)(((base + d.rng_origin) >> 2) + lane_quad<PAIRED, LOG2B>(j, k));
                     U4 r = mdq_philox4x32_10(U4{(uint32_t)q, (uint32_t)(q >> 32), d.tensor_id, d.step},
                                              (uint32_t)seed, (uint32_t)(seed >> 32));
                     const uint32_t w[4] = {r.x, r.y, r.z, r.w};
@@ -728,7 +730,7 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
             } else {
 #pragma unroll
                 for (int e = 0; e < EPL; ++e) {
-                    const uint64_t idx = (uint64_t)(base + e);
+                    const uint64_t idx = (uint64_t)(base + d.rng_origin + e);
                     const uint64_t q = idx >> 2;
                     U4 r = mdq_philox4x32_10(U4{(uint32_t)q, (uint32_t)(q >> 32), d.tensor_id, d.step},
                                              (uint32_t)seed, (uint32_t)(seed >> 32));

@@ -119,9 +119,10 @@ class TensorState:
     eps: float
     weight_decay: float
     tensor_id: int = 0
+    elem_offset: int = 0        # element 0's index in tensor_id's stochastic-rounding stream
 
 
-# numpy mirror of ``stq_tensor`` (144 bytes, no padding): a plan's descriptor list
+# numpy mirror of ``stq_tensor`` (152 bytes, no padding): a plan's descriptor list
 # lives in one structured array whose columns are refreshed vectorised per step.
 STQ_TENSOR_DTYPE = np.dtype([
     ("p", np.uint64), ("grad", np.uint64), ("exp_avg", np.uint64), ("exp_avg_sq", np.uint64),
@@ -131,6 +132,7 @@ STQ_TENSOR_DTYPE = np.dtype([
     ("v_min_numel", np.int64),
     ("beta1", np.float32), ("beta2", np.float32), ("lr", np.float32), ("weight_decay", np.float32),
     ("eps", np.float32), ("step", np.int32), ("bits", np.int32), ("tensor_id", np.uint32),
+    ("elem_offset", np.int64),
 ])
 assert STQ_TENSOR_DTYPE.itemsize == ctypes.sizeof(StqTensor)
 
@@ -238,7 +240,7 @@ def _pack_entries(entries: Sequence[TensorState]):
             e.p.numel(), e.grad.numel(), e.exp_avg.numel(), e.exp_avg_sq.numel(),
             e.scale_m.numel(), e.scale_v.numel(), e.v_min.numel(),
             e.beta1, e.beta2, e.lr, e.weight_decay, e.eps, int(e.step), int(e.bits),
-            int(e.tensor_id) & 0xFFFFFFFF))
+            int(e.tensor_id) & 0xFFFFFFFF, int(e.elem_offset)))
     arr[:] = rows
     return arr, (dtype_code(gdt), dtype_code(eadt), dtype_code(easqdt))
 
@@ -263,7 +265,8 @@ def block_aligned_ranges(numel: int, block_size: int, world: int):
 
 def shard_states(entries: Sequence[TensorState], block_size: int, world: int, rank: int):
     """The TensorState views of piece ``rank`` of every tensor (block_aligned_ranges); tensors
-    whose piece is empty are left out."""
+    whose piece is empty are left out.  Each piece's ``elem_offset`` is its start in the tensor,
+    so stochastic rounding draws the whole tensor's random numbers too."""
     B = min(int(block_size), 1024)
     out = []
     for e in entries:
@@ -274,7 +277,7 @@ def shard_states(entries: Sequence[TensorState], block_size: int, world: int, ra
         vsq = e.exp_avg_sq if e.exp_avg_sq.numel() == 0 else e.exp_avg_sq.view(-1)[s:t]
         out.append(TensorState(e.p.view(-1)[s:t], e.grad.view(-1)[s:t], e.exp_avg.view(-1)[s:t], vsq,
                                e.scale_m[b0:b1], e.scale_v[b0:b1], e.v_min[b0:b1], e.step, e.bits, e.lr,
-                               e.beta1, e.beta2, e.eps, e.weight_decay, e.tensor_id))
+                               e.beta1, e.beta2, e.eps, e.weight_decay, e.tensor_id, e.elem_offset + s))
     return out
 
 

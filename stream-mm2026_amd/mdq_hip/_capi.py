@@ -75,6 +75,7 @@ class StqTensor(ctypes.Structure):
         ("step", ctypes.c_int32),
         ("bits", ctypes.c_int32),
         ("tensor_id", ctypes.c_uint32),
+        ("elem_offset", ctypes.c_int64),
     ]
 
 

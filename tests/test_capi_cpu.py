@@ -6,6 +6,7 @@ import os
 import re
 
 import pytest
+import torch
 
 import mdq_hip
 from mdq_hip import _capi
@@ -92,6 +93,32 @@ def test_multi_tensor_rejects_mixed_storage():
     # tensor 0 is packed4 (empty v codes), tensor 1 would be uint8+uint8: not a valid pair
     rc = L.stq_multi_tensor_mdq_adamw(arr, 2, 0, 3, 3, 128, 0, 0, None, 0, None)
     assert rc == _capi.STQ_ERR_INVALID and "MDQ: state must be packed4" in err()
+
+
+@pytest.mark.parametrize("off,block", [(-128, 128), (64, 128), (1, 2), (1000, 4096)])
+def test_multi_tensor_rejects_bad_elem_offset(off, block):
+    """elem_offset (a piece's start in its tensor's stochastic-rounding stream) must be >= 0 and a
+    multiple of min(block_size, 1024)."""
+    arr = (_capi.StqTensor * 1)()
+    s = arr[0]
+    s.p = s.grad = s.exp_avg = s.scale_m = s.scale_v = s.v_min = FAKE
+    s.numel = s.grad_numel = s.exp_avg_numel = 256
+    s.scale_m_numel = s.scale_v_numel = s.v_min_numel = 256
+    s.beta1, s.beta2, s.lr, s.weight_decay, s.eps = 0.9, 0.999, 1e-3, 0.0, 1e-8
+    s.step, s.bits, s.elem_offset = 1, 4, off
+    rc = mdq_hip.lib().stq_multi_tensor_mdq_adamw(arr, 1, 0, 3, 3, block, 1, 0, None, 0, None)
+    B = min(block, 1024)
+    assert rc == _capi.STQ_ERR_INVALID
+    assert f"elem_offset ({off}) must be >= 0 and a multiple of the block size {B}" in err()
+
+
+def test_shard_states_set_elem_offsets():
+    n, B, world = 1000, 64, 3
+    t = torch.zeros(n)
+    e = mdq_hip.TensorState(t, t, t.to(torch.uint8), torch.empty(0, dtype=torch.uint8), t[:16], t[:16], t[:16],
+                            1, 4, 1e-3, 0.9, 0.999, 1e-8, 0.0, 7, elem_offset=640)
+    got = [mdq_hip.shard_states([e], B, world, r)[0].elem_offset for r in range(world)]
+    assert got == [640 + s for s, _ in mdq_hip.block_aligned_ranges(n, B, world)] == [640, 640 + 384, 640 + 704]
 
 
 class StqCodeOut(ctypes.Structure):
