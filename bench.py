@@ -390,9 +390,21 @@ def transitions(reps: int):
     return out
 
 
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(gdt: str, bits: int, B: int, seconds: float):
     """The oracle (C, OpenMP over quant blocks) on a 2^24-param slice of the same
-    workload, repeated for about `seconds`; params/s over this host's cores."""
+    workload, repeated for about `seconds` on this host's cores, then for a third of
+    that on one thread; params/s."""
     import numpy as np
 
     from oracle import mdq_oracle as orc
@@ -405,17 +417,27 @@ def cpu_baseline(gdt: str, bits: int, B: int, seconds: float):
     storage = {4: orc.STORE_P4, 8: orc.STORE_S8, 16: orc.STORE_S16, 32: orc.STORE_S32}[bits]
     cm, cv, sm, sv, vm = orc.init_state(n, B, storage)
     cores = len(os.sched_getaffinity(0))
-    steps, t0 = 0, time.perf_counter()
-    while True:
-        orc.step(p, g, cm, cv, sm, sv, vm, beta1=0.9, beta2=0.999, lr=1e-3, weight_decay=0.01, eps=1e-8,
-                 step=steps + 1, bits=bits, block_size=B, storage=storage, threads=cores)
-        steps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
+    done = 0
+
+    def timed(threads, budget):
+        nonlocal done
+        steps, t0 = 0, time.perf_counter()
+        while True:
+            done += 1
+            orc.step(p, g, cm, cv, sm, sv, vm, beta1=0.9, beta2=0.999, lr=1e-3, weight_decay=0.01, eps=1e-8,
+                     step=done, bits=bits, block_size=B, storage=storage, threads=threads)
+            steps += 1
+            el = time.perf_counter() - t0
+            if el >= budget:
+                return steps, el
+
+    steps, el = timed(cores, seconds)
+    steps1, el1 = timed(1, seconds / 3)
     return dict(value=n * steps / el, unit="params/s", cores=cores, kind="port",
+                value_1thread=n * steps1 / el1, cpu_model=cpu_model(),
                 sample=f"{n} params ({gdt} grads, {bits}-bit codes, B={B}) x {steps} steps, "
-                       f"{el:.1f} s, oracle/mdq_oracle.c with {cores} OpenMP threads")
+                       f"{el:.1f} s, oracle/mdq_oracle.c with {cores} OpenMP threads; "
+                       f"1 thread: {steps1} steps, {el1:.1f} s")
 
 
 def main():
@@ -542,7 +564,8 @@ def main():
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle) ...")
         cpu = cpu_baseline(w["gdt"], w["bits"], w["B"], args.cpu_seconds)
-        log(f"cpu baseline: {cpu['value']:.3e} params/s on {cpu['cores']} cores")
+        log(f"cpu baseline: {cpu['value']:.3e} params/s on {cpu['cores']} cores, "
+            f"{cpu['value_1thread']:.3e} on 1 thread ({cpu['cpu_model']})")
 
     out = {
         "metric": (METRICS.get(args.config, f"optimizer params updated/sec + achieved HBM GB/s (% peak), "
