@@ -19,7 +19,7 @@
 extern "C" {
 #endif
 
-#define STQ_ABI_VERSION 1
+#define STQ_ABI_VERSION 2
 
 enum stq_status {
     STQ_OK = 0,
@@ -225,7 +225,10 @@ int stq_abi_version(void);
  * Device copies of the step's fp32 math, for checking it against a CPU
  * implementation (no reference counterpart: the reference calls CUDA libm).
  *   which = 0: e^x, 1: log x (x a positive normal, +inf or NaN).
- * stq_device_math: y[i] = f(x[i]) for device arrays x, y of n floats.
+ * stq_device_math: y[i] = f(x[i]) for device arrays x, y of n floats; or, for
+ *   which = 2 (n even), the step kernel's fast v-code map: for each pair
+ *   (x[2i], x[2i+1]) = (dv, vmin), dv a positive normal float,
+ *   (y[2i], y[2i+1]) = (ln 2 / dv, -vmin / dv) as the kernel computes them.
  * stq_device_math_digests: for the bit patterns first .. first+count-1, the
  *   sum over each chunk of mix64(bits(x) << 32 | bits(f(x))) into
  *   digests[ceil(count / chunk)] (device uint64, zeroed by the caller).
@@ -235,13 +238,15 @@ int stq_device_math_digests(int which, uint32_t first, uint32_t count, uint32_t 
                             uint64_t *digests, void *stream);
 
 /*
- * max over the floats with bit patterns first .. first+count-1 (positive and
- * finite) of |v_log_f32(x) * ln 2 - (the kernels' log x)|, computed in fp64 and
- * atomically max-ed, as the bit pattern of a double, into the device uint64
- * *max_err_bits (zeroed by the caller).  The step kernel's fast v-code path
- * relies on this bound (no reference counterpart).
+ * max(0, max over the floats x with bit patterns first .. first+count-1
+ * (positive and finite) of |v_log_f32(x) * ln 2 - l(x)| - slope * |l(x)|),
+ * l = the kernels' log, computed in fp64 and atomically max-ed, as the bit
+ * pattern of a double, into the device uint64 *max_err_bits (zeroed by the
+ * caller).  The step kernel's fast v-code path relies on this bound, with
+ * slope 0 and with the slope it uses (no reference counterpart).
  */
-int stq_device_log_approx_error(uint32_t first, uint32_t count, uint64_t *max_err_bits, void *stream);
+int stq_device_log_approx_error(uint32_t first, uint32_t count, double slope, uint64_t *max_err_bits,
+                                void *stream);
 
 /* Host (CPU) builds of the same inline functions the kernels use. */
 void stq_host_math(int which, const float *x, float *y, int64_t n);

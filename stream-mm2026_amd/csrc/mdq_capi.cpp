@@ -670,18 +670,21 @@ int stq_abi_version(void) { return STQ_ABI_VERSION; }
 int stq_device_math(int which, const float *x, float *y, int64_t n, void *stream)
 {
     g_err.clear();
-    if (which != 0 && which != 1) return fail(STQ_ERR_INVALID, "which must be 0 (exp) or 1 (log)");
-    if (n < 0 || (n > 0 && (!x || !y))) return fail(STQ_ERR_INVALID, "bad arrays");
+    if (which < 0 || which > 2) return fail(STQ_ERR_INVALID, "which must be 0 (exp), 1 (log) or 2 (v-code map)");
+    if (n < 0 || (n > 0 && (!x || !y)) || (which == 2 && n % 2)) return fail(STQ_ERR_INVALID, "bad arrays");
     hipError_t e = mdq::launch_math(which, x, y, n, reinterpret_cast<hipStream_t>(stream));
     return e == hipSuccess ? STQ_OK : hip_fail(e, "math kernel launch");
 }
 
-int stq_device_log_approx_error(uint32_t first, uint32_t count, uint64_t *max_err_bits, void *stream)
+int stq_device_log_approx_error(uint32_t first, uint32_t count, double slope, uint64_t *max_err_bits,
+                                void *stream)
 {
     g_err.clear();
     if ((uint64_t)first + count > 0x100000000ull) return fail(STQ_ERR_INVALID, "range exceeds 2^32");
     if (count > 0 && !max_err_bits) return fail(STQ_ERR_INVALID, "null output");
-    hipError_t e = mdq::launch_log_approx_err(first, count, reinterpret_cast<unsigned long long *>(max_err_bits),
+    if (!(slope >= 0.0)) return fail(STQ_ERR_INVALID, "slope must be >= 0");
+    hipError_t e = mdq::launch_log_approx_err(first, count, slope,
+                                              reinterpret_cast<unsigned long long *>(max_err_bits),
                                               reinterpret_cast<hipStream_t>(stream));
     return e == hipSuccess ? STQ_OK : hip_fail(e, "log error kernel launch");
 }

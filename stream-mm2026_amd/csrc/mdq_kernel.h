@@ -33,10 +33,15 @@
 
 namespace mdq {
 
-// Bound on |v_log_f32(x) * ln 2 - mdq_logf(x)| over every float x in
-// [1e-12, FLT_MAX]: measured 9.114e-6 on gfx950 (stq_device_log_approx_error,
-// all inputs); the kernel uses 1.75 times that.
-#define MDQ_LOG_APPROX_ERR 1.6e-5f
+// |v_log_f32(x) * ln 2 - mdq_logf(x)| <= MDQ_LOG_APPROX_ERR + MDQ_LOG_APPROX_SLOPE *
+// |mdq_logf(x)| for every float x in [1e-12, FLT_MAX].  Measured on gfx950 over
+// all those inputs (stq_device_log_approx_error): the difference never exceeds
+// 1.8e-7 |mdq_logf(x)|, and 9.114e-6 in absolute terms.
+#define MDQ_LOG_APPROX_SLOPE 2.0e-7f
+#define MDQ_LOG_APPROX_ERR 2.5e-7f
+// Relative error bound of the fast v-code path's c1 + that of its c0 (each
+// within 2^-24 (1 + 2^-16) of the exact quotient; mdq_vcode_map).
+#define MDQ_VCODE_MAP_ERR 1.3e-7f
 
 template <int LOG2B>
 struct Cfg {
@@ -743,15 +748,15 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
             if (fastv) {
                 // The exact code is floor(T), T = fl(fma(u, fl(1/dv), uv)), u = fl(log x - vmin).
                 // Z = fl(z + uv) with z = fl(log2_hw(x) * c1 + c0) as in the nearest path
-                // differs from T by at most E + 4 (QV + 2) 2^-24 (E: the nearest path's bound;
-                // the rest: the roundings of u / dv vs u * fl(1/dv), of T and of Z).  Where Z is
-                // farther than that from an integer, floor(Z) is the code; the other elements
-                // take the exact path.
-                const float r = __builtin_amdgcn_rcpf(dv);
-                const float c1 = 0.69314718f * r;
-                const float c0 = -s_vmin * r;
+                // differs from T by at most G / dv + 5 (QV + 2) 2^-24 (G / dv: the nearest
+                // path's log and c1 / c0 term; the rest: the roundings of u, of z, of
+                // u / dv vs u * fl(1/dv), of T and of Z).  Where Z is farther than that from an
+                // integer, floor(Z) is the code; the other elements take the exact path.
+                const VCodeMap vmap = mdq_vcode_map(dv, s_vmin);
+                const float r = vmap.r, c1 = vmap.c1, c0 = vmap.c0;
                 const float L = fmaxf(fabsf(lmax), fabsf(lmin));
-                const float ep = (fma_(L, 1.3e-6f, MDQ_LOG_APPROX_ERR) * r + fma_(d.qvf + 2.0f, 2.4e-7f, 0.0f)) *
+                const float ep = (fma_(L, MDQ_LOG_APPROX_SLOPE + MDQ_VCODE_MAP_ERR, MDQ_LOG_APPROX_ERR) * r +
+                                  fma_(d.qvf + 2.0f, 3.0e-7f, 0.0f)) *
                                  1.001f;
                 bool redo[EPL];
                 bool any = false;
@@ -783,20 +788,24 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
             const float ilv = mdq_inv_lo(__builtin_amdgcn_rcpf(dv));
             if (fastv) {
                 // The exact code is K = round-half-away(u / dv), u = fl(log x - vmin).
-                // z = fl(log2_hw(x) * c1 + c0) with c1 = ln2 / dv and c0 = -vmin / dv, each
-                // from one hardware reciprocal r (up to 4 ulp off: c1, c0 within 1.25 * 2^-21
-                // relative), differs from u / dv by at most
-                // E = (A + 1.3e-6 L) / dv + (QV + 1) 2^-24, where A bounds
-                // |log2_hw(x) ln 2 - log x| over every float x >= 1e-12 (MDQ_LOG_APPROX_ERR,
-                // measured exhaustively on the device) and L = max(|lmax|, |lmin|).  Where z is
-                // farther than E + 2^-16 from a half-integer, floor(z + 1/2) is K (the 2^-16
-                // covers the rounding of z + 1/2 below 512); the other elements take the exact
-                // path.
-                const float r = __builtin_amdgcn_rcpf(dv);
-                const float c1 = 0.69314718f * r;
-                const float c0 = -s_vmin * r;
+                // z = fl(log2_hw(x) * c1 + c0), with c1 = ln 2 / dv and c0 = -vmin / dv each
+                // within 2^-24 (1 + 2^-16) relative (mdq_vcode_map), differs from u / dv by at
+                // most E = G / dv + 2 (QV + 1) 2^-24, G = A + (S + 1.3e-7) L: A + S |log x|
+                // bounds |log2_hw(x) ln 2 - log x| for every float x >= 1e-12
+                // (MDQ_LOG_APPROX_ERR, MDQ_LOG_APPROX_SLOPE, measured exhaustively on the
+                // device), L = max(|lmax|, |lmin|) >= |log x| within the block, 1.3e-7 L / dv
+                // bounds the errors of c1 and c0 times |log2_hw(x) ln 2| and |vmin|, and the
+                // last term the roundings of u and of z (z < QV + 1).  Where z is farther than
+                // E from a half-integer, floor(z + 1/2) is K.  The test compares z with
+                // kv = floor(fl(z + 1/2)) itself, so a rounding of z + 1/2 across an integer
+                // only sends the element to the exact path, as do all other elements within E
+                // of a half-integer.  The factor 1.001 covers r vs 1 / dv.
+                const VCodeMap vmap = mdq_vcode_map(dv, s_vmin);
+                const float r = vmap.r, c1 = vmap.c1, c0 = vmap.c0;
                 const float L = fmaxf(fabsf(lmax), fabsf(lmin));
-                const float ep = (fma_(L, 1.3e-6f, MDQ_LOG_APPROX_ERR) * r + fma_(d.qvf, 6.0e-8f, 1.6e-5f)) * 1.001f;
+                const float ep = (fma_(L, MDQ_LOG_APPROX_SLOPE + MDQ_VCODE_MAP_ERR, MDQ_LOG_APPROX_ERR) * r +
+                                  fma_(d.qvf + 1.0f, 1.2e-7f, 0.0f)) *
+                                 1.001f;
                 const float near = 0.5f - ep;
                 bool redo[EPL];
                 bool any = false;

@@ -24,6 +24,7 @@ hipError_t launch_tr_s32(int src, const MdqDesc *, int, long long, int, int, boo
 hipError_t launch_math(int which, const float *x, float *y, long long n, hipStream_t s);
 hipError_t launch_math_digests(int which, unsigned first, unsigned count, unsigned chunk,
                                unsigned long long *dig, hipStream_t s);
-hipError_t launch_log_approx_err(unsigned first, unsigned count, unsigned long long *out, hipStream_t s);
+hipError_t launch_log_approx_err(unsigned first, unsigned count, double slope, unsigned long long *out,
+                                 hipStream_t s);
 
 }  // namespace mdq

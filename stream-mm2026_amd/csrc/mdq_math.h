@@ -99,6 +99,30 @@ MDQ_HD float mdq_logf(float x)
     return ix >= 0x7f800000u ? x : res;
 }
 
+#if defined(__HIPCC__)
+// c1 = ln 2 / dv and c0 = -vmin / dv of the fast v-code path (a v code is
+// about log2_hw(x) * c1 + c0), each within 2^-24 (1 + 2^-16) relative of the
+// exact quotient.  r = v_rcp_f32(dv) is within a few ulp of 1/dv; q = a * r,
+// and one residual step q + fma(-q, dv, a) * r leaves an error far below an
+// ulp before the final rounding (for ln 2 the residual also adds
+// ln 2 - RN(ln 2)).  dv must be a positive normal float.
+struct VCodeMap {
+    float r, c1, c0;
+};
+__device__ __forceinline__ VCodeMap mdq_vcode_map(float dv, float vmin)
+{
+    const float r = __builtin_amdgcn_rcpf(dv);
+    const float ln2_hi = bits_f(0x3f317218u);                // RN(ln 2)
+    const float ln2_lo = bits_f(0xb102e308u);                // RN(ln 2 - ln2_hi)
+    const float q1 = ln2_hi * r;
+    const float c1 = fma_(fma_(-q1, dv, ln2_hi) + ln2_lo, r, q1);
+    const float a = -vmin;
+    const float q0 = a * r;
+    const float c0 = fma_(fma_(-q0, dv, a), r, q0);
+    return {r, c1, c0};
+}
+#endif
+
 // K = floor(u/d + 1/2) for u >= 0 and d a positive normal float, i.e.
 // round-half-away(u/d), computed exactly in fp32 as long as u/d < 2^19.
 // inv_lo must lie below 1/d by a relative 2^-23 .. 2^-20 (the kernel takes

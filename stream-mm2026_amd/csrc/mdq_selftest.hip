@@ -15,6 +15,15 @@ __device__ __forceinline__ float eval_math(int which, float x)
 __global__ __launch_bounds__(256) void math_kernel(int which, const float *__restrict__ x,
                                                    float *__restrict__ y, long long n)
 {
+    if (which == 2) {   // (dv, vmin) pairs -> (c1, c0) pairs of the fast v-code path
+        for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n / 2;
+             i += (long long)gridDim.x * blockDim.x) {
+            const VCodeMap m = mdq_vcode_map(x[2 * i], x[2 * i + 1]);
+            y[2 * i] = m.c1;
+            y[2 * i + 1] = m.c0;
+        }
+        return;
+    }
     for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (long long)gridDim.x * blockDim.x)
         y[i] = eval_math(which, x[i]);
@@ -47,16 +56,18 @@ __global__ __launch_bounds__(256) void math_digest_kernel(int which, unsigned fi
     }
 }
 
-// max over x = bits_f(first .. first+count-1) of |log2_hw(x) * ln 2 - mdq_logf(x)| in fp64,
-// as the bit pattern of a non-negative double (atomic max over uint64 orders those).
-__global__ __launch_bounds__(256) void log_approx_err_kernel(unsigned first, unsigned count,
+// max(0, max over x = bits_f(first .. first+count-1) of
+// |log2_hw(x) * ln 2 - mdq_logf(x)| - slope * |mdq_logf(x)|) in fp64, as the bit pattern
+// of a non-negative double (atomic max over uint64 orders those).
+__global__ __launch_bounds__(256) void log_approx_err_kernel(unsigned first, unsigned count, double slope,
                                                              unsigned long long *__restrict__ out)
 {
     double m = 0.0;
     for (unsigned long long i = (unsigned long long)blockIdx.x * blockDim.x + threadIdx.x; i < count;
          i += (unsigned long long)gridDim.x * blockDim.x) {
         const float x = bits_f(first + (unsigned)i);
-        const double e = fabs((double)__builtin_amdgcn_logf(x) * 0.69314718055994530942 - (double)mdq_logf(x));
+        const double l = (double)mdq_logf(x);
+        const double e = fabs((double)__builtin_amdgcn_logf(x) * 0.69314718055994530942 - l) - slope * fabs(l);
         m = e > m ? e : m;
     }
 #pragma unroll
@@ -67,12 +78,13 @@ __global__ __launch_bounds__(256) void log_approx_err_kernel(unsigned first, uns
     if ((threadIdx.x & 63) == 0) atomicMax(out, (unsigned long long)__double_as_longlong(m));
 }
 
-hipError_t launch_log_approx_err(unsigned first, unsigned count, unsigned long long *out, hipStream_t s)
+hipError_t launch_log_approx_err(unsigned first, unsigned count, double slope, unsigned long long *out,
+                                 hipStream_t s)
 {
     if (count == 0) return hipSuccess;
     unsigned long long blocks = ((unsigned long long)count + 255) / 256;
     int grid = (int)(blocks < 65536 ? blocks : 65536);
-    hipLaunchKernelGGL(log_approx_err_kernel, dim3(grid), dim3(256), 0, s, first, count, out);
+    hipLaunchKernelGGL(log_approx_err_kernel, dim3(grid), dim3(256), 0, s, first, count, slope, out);
     return hipGetLastError();
 }
 

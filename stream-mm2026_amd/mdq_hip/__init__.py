@@ -421,23 +421,27 @@ def convert_codes(items) -> None:
         check(lib().stq_multi_tensor_convert_codes(arr.ctypes.data, len(items), _capi.stream_handle(dev)))
 
 
-def device_log_approx_error(first: int, count: int, device="cuda:0") -> float:
-    """max |v_log_f32(x) ln 2 - log x| over the floats with bit patterns first .. first+count-1,
-    computed on the device in fp64 (the bound behind the step kernel's fast v-code path)."""
+def device_log_approx_error(first: int, count: int, slope: float = 0.0, device="cuda:0") -> float:
+    """max(0, max |v_log_f32(x) ln 2 - log x| - slope |log x|) over the floats with bit patterns
+    first .. first+count-1, computed on the device in fp64 (the bound behind the step kernel's
+    fast v-code path)."""
     dev = torch.device(device)
     out = torch.zeros(1, dtype=torch.int64, device=dev)
     with torch.cuda.device(dev):
-        check(lib().stq_device_log_approx_error(int(first), int(count), out.data_ptr(), _capi.stream_handle(dev)))
+        check(lib().stq_device_log_approx_error(int(first), int(count), float(slope), out.data_ptr(),
+                                                _capi.stream_handle(dev)))
     return float(out.cpu().view(torch.float64).item())
 
 
 def device_math(which: str, x: torch.Tensor) -> torch.Tensor:
-    """Device e^x (``which='exp'``) or log x (``'log'``) with the kernels' own fp32 code."""
+    """Device e^x (``which='exp'``) or log x (``'log'``) with the kernels' own fp32 code; or
+    ``'vcode_map'``: x holds (dv, vmin) pairs, the result the fast v-code path's
+    (ln 2 / dv, -vmin / dv) pairs."""
     assert x.is_cuda and x.dtype == torch.float32 and x.is_contiguous()
     y = torch.empty_like(x)
+    code = {"exp": 0, "log": 1, "vcode_map": 2}[which]
     with torch.cuda.device(x.device):
-        check(lib().stq_device_math(0 if which == "exp" else 1, _ptr(x), _ptr(y), x.numel(),
-                                    _capi.stream_handle(x.device)))
+        check(lib().stq_device_math(code, _ptr(x), _ptr(y), x.numel(), _capi.stream_handle(x.device)))
     return y
 
 

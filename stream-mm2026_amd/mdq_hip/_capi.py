@@ -49,6 +49,10 @@ EXPORTED_SYMBOLS = (
 )
 
 
+# STQ_ABI_VERSION of include/stquant_hip.h this package is written against
+ABI_VERSION = 2
+
+
 class StqTensor(ctypes.Structure):
     """Mirror of ``stq_tensor``."""
 
@@ -123,7 +127,7 @@ def lib() -> ctypes.CDLL:
     L.stq_device_math.restype = ctypes.c_int
     L.stq_device_math_digests.argtypes = [i32, u32, u32, u32, vp, vp]
     L.stq_device_math_digests.restype = ctypes.c_int
-    L.stq_device_log_approx_error.argtypes = [u32, u32, vp, vp]
+    L.stq_device_log_approx_error.argtypes = [u32, u32, ctypes.c_double, vp, vp]
     L.stq_device_log_approx_error.restype = ctypes.c_int
     L.stq_host_math.argtypes = [i32, vp, vp, i64]
     L.stq_host_math.restype = None
@@ -133,6 +137,9 @@ def lib() -> ctypes.CDLL:
     L.stq_host_div_code_range.restype = None
     L.stq_host_philox4x32_10.argtypes = [vp, vp, vp]
     L.stq_host_philox4x32_10.restype = None
+    if L.stq_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"{LIB_PATH} has ABI version {L.stq_abi_version()}, this package needs "
+                           f"{ABI_VERSION}: rebuild it")
     _lib = L
     return L
 
