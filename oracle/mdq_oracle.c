@@ -269,12 +269,13 @@ int mdq_oracle_step(const mdqo_tensor *t, const mdqo_hparams *h)
                     l = mdq_oracle_logf(v + 1e-12f);
                     mv[i] = m; vv[i] = v; lv[i] = l;
                 }
-                /* block reductions :95-97 (order-free: max/min are exact) */
+                /* block reductions :95-97 with fmaxf / fminf (:26-50): NaN is ignored
+                 * unless every lane is NaN; otherwise order-free (max/min are exact) */
                 if (first) { max_m = a; max_lv = l; min_lv = l; first = 0; }
                 else {
-                    max_m = a > max_m ? a : max_m;
-                    max_lv = l > max_lv ? l : max_lv;
-                    min_lv = l < min_lv ? l : min_lv;
+                    max_m = fmaxf(max_m, a);
+                    max_lv = fmaxf(max_lv, l);
+                    min_lv = fminf(min_lv, l);
                 }
             }
             /* new scales :101-106 */
@@ -301,6 +302,12 @@ int mdq_oracle_step(const mdqo_tensor *t, const mdqo_hparams *h)
                     qm = round((double)m / (double)dm);            /* :113 */
                     qv = round((double)(l - s_vmin) / (double)dv); /* :123 */
                 }
+                /* A NaN quotient (NaN or infinite m or log v over an infinite or NaN
+                 * scale) passes the clamps below and reaches the reference's (int)
+                 * conversion (:118,126), which gives 0 on its target (PTX cvt maps NaN
+                 * to 0); C leaves that conversion undefined, so it is spelled out. */
+                if (qm != qm) qm = 0.0;
+                if (qv != qv) qv = 0.0;
                 if (qm < -qlm) qm = -qlm;                           /* :114-117 */
                 if (qm > qlm - 1.0) qm = qlm - 1.0;
                 if (qv < 0.0) qv = 0.0;                             /* :124-125 */

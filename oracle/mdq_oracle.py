@@ -25,6 +25,11 @@ v codes / scale_v      min-log element -> 0, max-log element -> 2^bits-1, tail l
 AdamW update           bits=32: matches a float64 textbook AdamW with v0 = e^-20 to
                        1e-6; lr=0 leaves p; g=0 state=0 gives p*(1-lr*wd) exactly
 stochastic rounding    unbiasedness and code histogram (tests/test_oracle_step.py)
+NaN / inf grads        the reference's fmaxf / fminf reductions ignore NaN and its (int)
+                       conversion maps NaN to 0: a NaN element leaves its block's scales
+                       and other codes as a finite stand-in does, codes 0, p NaN; an inf
+                       element gives inf scales and all-zero codes; an all-NaN block NaN
+                       scales (tests/test_oracle_nonfinite.py)
 grad statistics        the reference's own torch expression (stquant_opt_simple.py:93-98)
                        on CPU tensors, closed forms for constant / two-valued grads,
                        numel 0 / 1 NaN cases (tests/test_oracle_grad_stats.py)

@@ -655,9 +655,12 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
             if (e == 0) { amax = a; lmax = l; lmin = l; }
             else { amax = fmaxf(amax, a); lmax = fmaxf(lmax, l); lmin = fminf(lmin, l); }
         }
-        ka = __builtin_bit_cast(int32_t, amax);
-        kx = f2key(lmax);
-        kn = f2key(lmin);
+        // The reference reduces with fmaxf / fminf (:26-50), which skip NaN:
+        // fmaxf / fminf above do so within the lane, and a lane left with NaN
+        // (all its elements NaN) offers a key every other lane beats.
+        ka = amax == amax ? __builtin_bit_cast(int32_t, amax) : -1;
+        kx = lmax == lmax ? f2key(lmax) : INT32_MIN;
+        kn = lmin == lmin ? f2key(lmin) : INT32_MAX;
     }
     if constexpr (LPB <= 64) {
         ka = group_reduce<LPB, true>(ka);
@@ -688,8 +691,11 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
             lmin = mdq_logf(__builtin_bit_cast(float, kn));
         }
     } else {
-        lmax = key2f(kx);
-        lmin = key2f(kn);
+        // keys no lane beat: every element of the block is NaN (NaN scales, as
+        // fmaxf of NaN only)
+        if (ka < 0) amax = __builtin_nanf("");
+        lmax = kx == INT32_MIN ? __builtin_nanf("") : key2f(kx);
+        lmin = kn == INT32_MAX ? __builtin_nanf("") : key2f(kn);
     }
 
     // new scales (:101-106)
@@ -776,10 +782,13 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
                         if (redo[e]) qvf[e] = floor_(fma_(mdq_logf(v[e] + 1e-12f) - s_vmin, inv_dv, uv[e]));
                 }
             } else {
+                // non-finite quotients give code 0, as in the nearest path below
+                const bool sm_fin = dm <= __FLT_MAX__, sv_fin = dv <= __FLT_MAX__;
 #pragma unroll
                 for (int e = 0; e < EPL; ++e) {
-                    qmf[e] = floor_(fma_(m[e], inv_dm, um[e]));
-                    qvf[e] = floor_(fma_(lv[e] - s_vmin, inv_dv, uv[e]));
+                    const float u = lv[e] - s_vmin;
+                    qmf[e] = sm_fin && fabsf(m[e]) <= __FLT_MAX__ ? floor_(fma_(m[e], inv_dm, um[e])) : 0.0f;
+                    qvf[e] = sv_fin && u <= __FLT_MAX__ ? floor_(fma_(u, inv_dv, uv[e])) : 0.0f;
                 }
             }
         } else {
@@ -825,11 +834,18 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
                         if (redo[e]) qvf[e] = mdq_round_half_away(mdq_logf(v[e] + 1e-12f) - s_vmin, dv, ilv, hdv);
                 }
             } else {
+                // A quotient that is no finite number (a NaN or infinite m or log v, or a
+                // NaN or infinite scale) reaches the reference's (int) conversion as NaN,
+                // which gives 0 on its target (PTX cvt maps NaN to 0); finite / inf is 0
+                // as well (:113-127).  The fast path runs only when every v, and so every
+                // m and both scales, is finite.
+                const bool sm_fin = dm <= __FLT_MAX__, sv_fin = dv <= __FLT_MAX__;
 #pragma unroll
                 for (int e = 0; e < EPL; ++e) {
                     const float K = mdq_round_half_away(fabsf(m[e]), dm, ilm, hdm);
-                    qmf[e] = __builtin_copysignf(K, m[e]);
-                    qvf[e] = mdq_round_half_away(lv[e] - s_vmin, dv, ilv, hdv);
+                    const float u = lv[e] - s_vmin;
+                    qmf[e] = sm_fin && fabsf(m[e]) <= __FLT_MAX__ ? __builtin_copysignf(K, m[e]) : 0.0f;
+                    qvf[e] = sv_fin && u <= __FLT_MAX__ ? mdq_round_half_away(u, dv, ilv, hdv) : 0.0f;
                 }
             }
         }
@@ -850,10 +866,13 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
         const double qlv = __builtin_ldexp(1.0, (int)d.bits) - 1.0;
 #pragma unroll
         for (int e = 0; e < EPL; ++e) {
+            // a NaN quotient converts to 0 (the reference's (int) of NaN on its target)
             double qm_ = __builtin_round((double)m[e] / (double)dm);
+            qm_ = qm_ == qm_ ? qm_ : 0.0;
             qm_ = qm_ < -qlm ? -qlm : qm_;
             qm_ = qm_ > qlm - 1.0 ? qlm - 1.0 : qm_;
             double qv_ = __builtin_round((double)(lv[e] - s_vmin) / (double)dv);
+            qv_ = qv_ == qv_ ? qv_ : 0.0;
             qv_ = qv_ < 0.0 ? 0.0 : qv_;
             qv_ = qv_ > qlv ? qlv : qv_;
             qmi[e] = (int32_t)qm_;
@@ -923,6 +942,11 @@ __global__ __launch_bounds__(Cfg<LOG2B>::THREADS) void mdq_step_kernel(const Mdq
                                                                       unsigned long long seed)
 {
     using C = Cfg<LOG2B>;
+    // Occupancy cap at 7 waves per SIMD: the clobber reserves v0..v71, so the
+    // register file never holds 8 of these waves.  With 8 (64 VGPRs or fewer)
+    // the LLaMA 4-bit step ran 1 % slower (same-allocation A/B 13.36 vs
+    // 13.23 ms): more requests in flight than the HBM streams profit from.
+    asm volatile("" ::: "v71");
     constexpr bool USE_LUT = (SRC == ST_P4) && C::B >= 32;
     __shared__ float lut_s[USE_LUT ? C::TB * 16 : 1];
     __shared__ int32_t xw_s[6];

@@ -142,12 +142,13 @@ MDQ_HD float mdq_round_half_away(float u, float d, float inv_lo, float hd)
 // x / D correctly rounded for D = (float)(2^bits - 1), bits 1..32, given
 // y = RN(1/D): q = x*y is within an ulp, the fma residual x - q*D is exact,
 // and one correction q + r*y rounds to RN(x/D).  Checked against IEEE
-// division for every positive float x and every bits value.
+// division for every positive float x and every bits value.  For x = +inf
+// the residual is NaN and q = +inf is the quotient; NaN stays NaN.
 MDQ_HD float mdq_div_code_range(float x, float D, float y)
 {
     const float q = x * y;
     const float r = fma_(-q, D, x);
-    return fma_(r, y, q);
+    return r == r ? fma_(r, y, q) : q;
 }
 
 // The reciprocal of d stepped down by 4 ulp, for mdq_round_half_away.

@@ -1,63 +1,102 @@
-"""Non-finite gradients on the GPU.  The reference's codes for a block holding inf / NaN values
-are undefined (a NaN quotient goes through a double -> int cast, stquant_kernel.cu:113-131), so
-those blocks are not compared.  What must hold: every block without a non-finite value keeps
-bit-exact codes and scales and matching params, whichever kernel path its tile takes (a tile
-with a non-finite value takes the exact path, its neighbours the fast one), and the launch
-completes normally."""
+"""NaN and infinite gradients: the step kernels against the oracle, through the C ABI.
+
+The reference reduces each block with fmaxf / fminf (stquant_kernel.cu:26-50), which skip NaN,
+and converts a NaN quotient to code 0 (:113-127); tests/test_oracle_nonfinite.py pins the oracle
+to that.  Here grads carry NaN, +inf and -inf elements and whole NaN blocks in the first half of
+each tensor (the second half stays finite, so fast-path tiles run beside slow-path ones), over
+three consecutive steps: blocks that saw an infinity decode to NaN on the next step, as in the
+reference.  Codes must be bit-exact, the three scale arrays bit-exact or NaN where the oracle's
+are, params NaN where the oracle's are and within the parity bar elsewhere.
+"""
 import numpy as np
 import pytest
 import torch
 
 import mdq_hip
 from oracle import mdq_oracle as orc
-from test_gpu_parity import DEV, HP, STORE_TORCH, to_dev
+from test_gpu_parity import Case, assert_bits_equal, assert_params_close, resync_params
 
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("storage,bits,B,rounding", [(orc.STORE_P4, 4, 128, "nearest"),
-                                                     (orc.STORE_S8, 8, 64, "nearest"),
-                                                     (orc.STORE_S8, 8, 256, "stochastic")])
-def test_nonfinite_grads_leave_finite_blocks_exact(storage, bits, B, rounding):
-    print(f"case: non-finite grads storage={storage} bits={bits} B={B} {rounding}", flush=True)
-    n = 1 << 18
-    rng = np.random.default_rng(5)
-    p = (rng.standard_normal(n) * 0.02).astype(np.float32)
-    cm, cv, sm, sv, vm = orc.init_state(n, B, storage)
-    dm, dv = STORE_TORCH[storage]
-    tp, tcm, tsm, tsv, tvm = (to_dev(a.copy()) for a in (p, cm, sm, sv, vm))
-    tcv = to_dev(cv.copy()) if cv is not None else torch.empty(0, dtype=torch.uint8, device=DEV)
-    rnd = orc.ROUND_STOCHASTIC if rounding == "stochastic" else orc.ROUND_NEAREST
-    bad_blocks = set()
+def assert_floats_equal_or_nan(name, t, a):
+    got = t.cpu().numpy()
+    nan_g, nan_a = np.isnan(got), np.isnan(a)
+    assert np.array_equal(nan_g, nan_a), f"{name}: NaN at {np.nonzero(nan_g != nan_a)[0][:5]} differs"
+    assert np.array_equal(got[~nan_g].view(np.uint32), a[~nan_a].view(np.uint32)), f"{name} differs"
+
+
+class NonfiniteCase(Case):
+    def grads(self, rng):
+        g = (rng.standard_normal(self.n) * 1e-3).astype(np.float32)
+        half = self.n // 2
+        r = rng.random(half)
+        g[:half][r < 0.004] = np.nan
+        g[:half][(r >= 0.004) & (r < 0.006)] = np.inf
+        g[:half][(r >= 0.006) & (r < 0.008)] = -np.inf
+        nb = max(1, half // self.B)
+        for b in rng.choice(nb, size=max(1, nb // 20), replace=False):
+            g[b * self.B:min((b + 1) * self.B, half)] = np.nan
+        if self.grad_dtype == "bf16":
+            tg = torch.from_numpy(g).to(torch.bfloat16)
+            return tg.view(torch.int16).numpy().view(np.uint16).copy(), tg.to("cuda:0")
+        return g, torch.from_numpy(g).to("cuda:0")
+
+    def check(self, p_prev):
+        torch.cuda.synchronize()
+        cm, cv, sm, sv, vm = self.state
+        assert_bits_equal("exp_avg", self.tcm, cm)
+        if cv is not None:
+            assert_bits_equal("exp_avg_sq", self.tcv, cv)
+        for name, t, a in (("scale_m", self.tsm, sm), ("scale_v", self.tsv, sv), ("v_min", self.tvm, vm)):
+            assert_floats_equal_or_nan(name, t, a)
+        got = self.tp.cpu().numpy()
+        nan_g, nan_a = np.isnan(got), np.isnan(self.p)
+        assert np.array_equal(nan_g, nan_a), f"params: NaN at {np.nonzero(nan_g != nan_a)[0][:5]} differs"
+        fin = ~nan_a
+        assert_params_close(self.tp[torch.from_numpy(fin).to(self.tp.device)], self.p[fin], p_prev[fin])
+        resync_params(self.tp, self.p)
+
+
+STORAGES = [(orc.STORE_P4, 4), (orc.STORE_S8, 8), (orc.STORE_S8, 5), (orc.STORE_S16, 16), (orc.STORE_S16, 12),
+            (orc.STORE_S32, 32), (orc.STORE_S32, 20)]
+
+
+@pytest.mark.parametrize("B", [4, 128, 1024])
+@pytest.mark.parametrize("storage,bits", STORAGES)
+@pytest.mark.parametrize("rounding", [orc.ROUND_NEAREST, orc.ROUND_STOCHASTIC])
+def test_nonfinite_grads_match_oracle(storage, bits, B, rounding):
+    gdt = "bf16" if (bits + B) % 2 else np.float32
+    print(f"case: nonfinite storage={storage} bits={bits} B={B} rounding={rounding} grad={gdt}", flush=True)
+    rng = np.random.default_rng(1000 * storage + 10 * bits + B + 7 * rounding)
+    c = NonfiniteCase(B * 37 + 11, B, storage, rng, grad_dtype=gdt)
     for step in (1, 2, 3):
-        g = (rng.standard_normal(n) * 1e-3).astype(np.float32)
+        g, tg = c.grads(rng)
+        p_prev = c.p.copy()
+        c.oracle_step(g, step, bits, rounding=rounding, seed=3, tensor_id=1)
+        mdq_hip.multi_tensor_step([c.entry(tg, step, bits, tensor_id=1)], B,
+                                  rounding="stochastic" if rounding else "nearest", seed=3)
+        c.check(p_prev)
+
+
+@pytest.mark.parametrize("storage,bits,B,rounding", [(orc.STORE_P4, 4, 128, orc.ROUND_NEAREST),
+                                                     (orc.STORE_S8, 8, 64, orc.ROUND_NEAREST),
+                                                     (orc.STORE_S8, 8, 256, orc.ROUND_STOCHASTIC)])
+def test_nonfinite_at_one_step_then_finite(storage, bits, B, rounding):
+    """A few +-inf / NaN grads at step 2 of a 2^18-element tensor, finite grads before and after:
+    every block, those that held a non-finite value included, matches the oracle at every step."""
+    print(f"case: non-finite at step 2 storage={storage} bits={bits} B={B} rounding={rounding}", flush=True)
+    rng = np.random.default_rng(5)
+    c = Case(1 << 18, B, storage, rng)
+    for step in (1, 2, 3, 4):
+        g = (rng.standard_normal(c.n) * 1e-3).astype(np.float32)
         if step == 2:
-            idx = rng.choice(n, 12, replace=False)
+            idx = rng.choice(c.n, 12, replace=False)
             g[idx[:4]] = np.inf
             g[idx[4:8]] = -np.inf
             g[idx[8:]] = np.nan
-            bad_blocks |= set((idx // B).tolist())
-        orc.step(p, g.copy(), cm, cv, sm, sv, vm, step=step, bits=bits, block_size=B, storage=storage,
-                 rounding=rnd, seed=3, **HP)
-        e = mdq_hip.TensorState(tp, to_dev(g), tcm, tcv, tsm, tsv, tvm, step, bits, HP["lr"], HP["beta1"],
-                                HP["beta2"], HP["eps"], HP["weight_decay"], 0)
-        mdq_hip.multi_tensor_step([e], B, rounding=rounding, seed=3)
-        torch.cuda.synchronize()
-        good = np.ones(n // B, bool)
-        good[list(bad_blocks)] = False
-        ge = np.repeat(good, B)
-        assert np.array_equal(tcm.cpu().numpy()[ge], cm[ge]), f"m codes, step {step}"
-        if cv is not None:
-            assert np.array_equal(tcv.cpu().numpy()[ge], cv[ge]), f"v codes, step {step}"
-        for name, t, a in (("scale_m", tsm, sm), ("scale_v", tsv, sv), ("v_min", tvm, vm)):
-            assert np.array_equal(t.cpu().numpy()[good].view(np.uint32), a[good].view(np.uint32)), f"{name} {step}"
-        got = tp.cpu().numpy()
-        assert np.allclose(got[ge], p[ge], rtol=1e-5, atol=1e-9), f"params, step {step}"
-        # later steps start from identical state everywhere (the oracle's), so only the blocks
-        # that ever held a non-finite value stay excluded
-        tp.copy_(torch.from_numpy(p))
-        tcm.copy_(torch.from_numpy(cm))
-        if cv is not None:
-            tcv.copy_(torch.from_numpy(cv))
-        for t, a in ((tsm, sm), (tsv, sv), (tvm, vm)):
-            t.copy_(torch.from_numpy(a))
+        p_prev = c.p.copy()
+        c.oracle_step(g, step, bits, rounding=rounding, seed=3)
+        mdq_hip.multi_tensor_step([c.entry(torch.from_numpy(g).to("cuda:0"), step, bits)], B,
+                                  rounding="stochastic" if rounding else "nearest", seed=3)
+        NonfiniteCase.check(c, p_prev)

@@ -91,6 +91,8 @@ def test_new_v_scale_division_is_ieee(bits):
     method was adopted."""
     step = 997 if bits in (4, 8, 16, 32) else 99991
     x = np.arange(1, 0x7F800000, step, dtype=np.int64).astype(np.uint32).view(np.float32)
+    x = np.concatenate([x, np.array([np.inf, 0.0], np.float32)])   # an infinite log-v range too
     D = np.float32(2.0 ** bits - 1.0)
     got = mdq_hip.host_div_code_range(x, bits)
     assert np.array_equal(got.view(np.uint32), (x / D).astype(np.float32).view(np.uint32))
+    assert np.isnan(mdq_hip.host_div_code_range(np.array([np.nan], np.float32), bits)[0])
