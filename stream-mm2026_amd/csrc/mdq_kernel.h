@@ -18,7 +18,9 @@
 // * Block reductions (max|m|, max/min log v) run in registers, then across
 //   the LPB lanes with DPP row operations (quad_perm, row_half_mirror,
 //   row_mirror), ds_swizzle for 32 lanes, ds_bpermute for 64, and an LDS
-//   exchange between the two waves of a 1024-element block.
+//   exchange between the two waves of a 1024-element block.  They skip NaN as
+//   the reference's fmaxf / fminf trees do, and non-finite quotients give
+//   code 0, as its (int) conversion of NaN does.
 // * Packed 4-bit v codes dequantise through a 16-entry exp table per block
 //   built in LDS (16 exp per block instead of one per element).
 // * Requant uses mdq_round_half_away (exact fp32) for code widths <= 16 bits
