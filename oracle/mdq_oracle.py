@@ -32,7 +32,8 @@ NaN / inf grads        the reference's fmaxf / fminf reductions ignore NaN and i
                        scales (tests/test_oracle_nonfinite.py)
 grad statistics        the reference's own torch expression (stquant_opt_simple.py:93-98)
                        on CPU tensors, closed forms for constant / two-valued grads,
-                       numel 0 / 1 NaN cases (tests/test_oracle_grad_stats.py)
+                       numel 0 / 1 NaN cases, NaN / inf grads and overflowing squares
+                       (tests/test_oracle_grad_stats.py)
 =====================  ==============================================================
 
 Parity with the CUDA binary itself is unpinned at one boundary only: the ulp-level

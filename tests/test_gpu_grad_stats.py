@@ -2,7 +2,8 @@
 
 - ``mdq_hip.grad_stats`` against the oracle (float64 sums, tests/test_oracle_grad_stats.py)
   within 1e-6 relative, over ragged sizes (tile edges at 16384 and 32768), fp32/bf16/fp16 and
-  unaligned views; NaN where torch gives NaN (numel 0 and 1);
+  unaligned views; NaN where torch gives NaN (numel 0 and 1), NaN / inf where NaN / inf grads or
+  overflowing squares make them;
 - deterministic (bit-identical on repeat), and within 1e-5 of the reference's fp32 torch
   reductions run on the same device;
 - ``MDQAdamWSimple._scores`` (one [n] vector) bit-identical to the reference's per-tensor
@@ -48,6 +49,28 @@ def test_kernel_matches_oracle(dtype, offset):
         if v.numel() >= 2:
             tr = MDQAdamWSimple._compute_grad_stats(v.float()).cpu().numpy()
             np.testing.assert_allclose(got[i], tr, rtol=1e-5, atol=0, err_msg=f"torch, tensor {i}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_nonfinite_grads_match_oracle(dtype):
+    """NaN, +-inf and (fp32) overflowing squares in some tensors of a launch: the kernel gives the
+    oracle's NaN / inf entries (pinned to the reference's torch expression on the CPU), finite
+    entries within 1e-6, and the tensors without such values are unaffected."""
+    print(f"case: grad_stats non-finite {dtype}", flush=True)
+    vs = [v.clone() for v in views(dtype, 0, 3)]
+    vs[4][100] = float("nan")
+    vs[5][7] = float("inf")
+    vs[6][3], vs[6][9] = float("inf"), float("-inf")
+    vs[10][50] = float("-inf")
+    if dtype == torch.float32:
+        vs[11][2] = 3e38
+    got = mdq_hip.grad_stats(vs).cpu().numpy()
+    for i, v in enumerate(vs):
+        ref = orc.grad_stats(v.float().cpu().numpy())
+        assert np.array_equal(np.isnan(got[i]), np.isnan(ref)) and np.array_equal(np.isinf(got[i]), np.isinf(ref)), \
+            (i, got[i], ref)
+        fin = np.isfinite(ref)
+        np.testing.assert_allclose(got[i][fin], ref[fin], rtol=1e-6, atol=0, err_msg=f"tensor {i}")
 
 
 def test_mixed_dtypes_scatter_back():

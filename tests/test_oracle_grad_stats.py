@@ -40,3 +40,27 @@ def test_degenerate_sizes_follow_torch():
     assert one[0] == ref[0] == 3.0 and one[2] == ref[2] == 9.0
     assert np.isnan(one[1]) and np.isnan(ref[1])
     assert np.all(np.isnan(orc.grad_stats(np.zeros(0, np.float32))))
+
+
+NONFINITE = {
+    "nan": [(5, np.nan)],
+    "inf": [(7, np.inf)],
+    "-inf": [(7, -np.inf)],
+    "inf and -inf": [(3, np.inf), (9, -np.inf)],
+    "square overflows": [(2, 3e38)],
+}
+
+
+@pytest.mark.parametrize("case", list(NONFINITE))
+def test_nonfinite_grads_follow_torch(case):
+    """NaN / +-inf grads, and a grad whose square overflows fp32, give the NaN and inf entries
+    the reference's torch expression gives (a NaN grad: all NaN; an infinity: inf, NaN, inf;
+    an overflowing square: inf, finite, inf)."""
+    g = (np.random.default_rng(0).standard_normal(1000) * 1e-3).astype(np.float32)
+    for i, x in NONFINITE[case]:
+        g[i] = x
+    ref = MDQAdamWSimple._compute_grad_stats(torch.from_numpy(g)).numpy()
+    got = orc.grad_stats(g)
+    assert np.array_equal(np.isnan(got), np.isnan(ref)) and np.array_equal(np.isinf(got), np.isinf(ref)), (got, ref)
+    fin = np.isfinite(ref)
+    assert np.allclose(got[fin], ref[fin], rtol=2e-6, atol=0), (got, ref)
