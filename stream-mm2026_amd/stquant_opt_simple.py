@@ -17,7 +17,8 @@ reference's storage rules (:140-210).  Results per element are those of the
 reference kernel (:246-263 -> stquant_kernel.cu).
 
 New optional param-group keys (defaults keep the reference behaviour):
-``bits`` (fixed code width 4/8/16/32 instead of the score-based choice),
+``bits`` (fixed code width 4/8/16/32 instead of the score-based choice; such groups still
+count in the global gradient statistics that score the other groups),
 ``rounding`` ('nearest' or 'stochastic') and ``seed`` (stochastic stream).
 ``sync_timing=False`` skips the device synchronisations that fill the timing
 dict (and the kernel phase profile), so ``step()`` issues its work
@@ -735,11 +736,13 @@ class MDQAdamWSimple(Optimizer):
                 state = self.state[p]
                 self._init_state_if_needed(p, state, b_size)
 
-        # Fixed-width groups (new ``bits`` option) skip the score.
+        # Fixed-width groups (new ``bits`` option) take their width; tensors of the other groups
+        # are scored against global statistics over every tensor with a grad, as the reference
+        # computes them (it has no fixed groups).
         for p, group in params_with_grad:
             if group.get("bits") is not None:
                 self.state[p]["current_bit"] = int(group["bits"])
-        scored = all(g.get("bits") is None for _p, g in params_with_grad)
+        scored = any(g.get("bits") is None for _p, g in params_with_grad)
 
         grad_stats_ms = 0.0
         allreduce_ms = 0.0
@@ -782,9 +785,10 @@ class MDQAdamWSimple(Optimizer):
             states = [self.state[p] for p, _g in params_with_grad]
             scores = self._scores(stats_tensor, [st["step"] for st in states], tau)
             host_scores = scores.cpu().tolist()          # the step's one device -> host read
-            for st, sc, hs in zip(states, scores.unbind(0), host_scores):
+            for (_p, g), st, sc, hs in zip(params_with_grad, states, scores.unbind(0), host_scores):
                 st["last_score"] = sc
-                st["current_bit"] = self._score_to_bits(hs)
+                if g.get("bits") is None:
+                    st["current_bit"] = self._score_to_bits(hs)
             self._sync_device(dev)
             score_bits_ms = (time.perf_counter() - t_score) * 1000.0
 

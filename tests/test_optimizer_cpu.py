@@ -323,3 +323,24 @@ def test_steady_path_matches_slow_path(fast_cls, slow_cls):
     # change re-packs), 11-12 (set of params with grads changes), 13 (group config changes),
     # 15 and 18 (scored bit decisions), 16 (reload); steady everywhere else
     assert oa.steady_at == [3, 4, 5, 6, 8, 14, 17], oa.steady_at
+
+
+def test_mixed_fixed_and_scored_groups():
+    """A group with a fixed ``bits`` keeps its width while the other groups are scored, against
+    global statistics over every tensor with a grad: the scored tensors get the widths and scores
+    they get when the fixed group is scored too (same statistics, same step counts)."""
+    shapes = [(300,), (64, 9), (1000,), (37,)]
+    runs = []
+    for fixed in (False, True):
+        params = make_params(shapes, seed=5)
+        groups = [{"params": params[:2]}, {"params": params[2:], "bits": 4 if fixed else None}]
+        opt = SimpleCPU(groups, block_size=64)
+        for t in range(1, 4):
+            set_grads(params, 40 + t)
+            params[0].grad.mul_(100.0)           # a wide score spread: the scored widths differ
+            opt.step()
+        runs.append([(opt.state[p]["current_bit"], float(opt.state[p]["last_score"])) for p in params])
+    scored_free, scored_mixed = runs[0][:2], runs[1][:2]
+    assert scored_mixed == scored_free
+    assert [b for b, _s in runs[1][2:]] == [4, 4]
+    assert len({b for b, _s in runs[0]}) > 1
