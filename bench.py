@@ -68,6 +68,7 @@ def llama7b_flat_shapes():
 METRICS = {
     "llama7b": "optimizer params updated/sec + achieved HBM GB/s (% peak), LLaMA-7B shape, 1 GPU",
     "gpt2": "optimizer params updated/sec + achieved HBM GB/s (% peak), GPT-2 small shape, 1 GPU",
+    "flat4m": "optimizer params updated/sec, one flat 4,194,304-param tensor (cache-resident), 1 GPU",
 }
 
 CONFIGS = {
@@ -75,6 +76,9 @@ CONFIGS = {
     "llama7b": (llama7b_shapes, "bf16", 4, 128),
     "llama7b_flat": (llama7b_flat_shapes, "bf16", 4, 128),
     "gpt2": (gpt2_small_shapes, "f32", 4, 128),
+    # BASELINE config 1's tensor (59.5 MB of traffic per step: it stays in the 256 MB MALL, so
+    # its GB/s is no HBM roofline figure)
+    "flat4m": (lambda: [("flat", 4_194_304)], "f32", 4, 128),
 }
 
 
@@ -433,8 +437,10 @@ def cpu_baseline(gdt: str, bits: int, B: int, seconds: float):
 
     steps, el = timed(cores, seconds)
     steps1, el1 = timed(1, seconds / 3)
+    bpp = bytes_per_param(2 if gdt == "bf16" else 4, bits, B)
     return dict(value=n * steps / el, unit="params/s", cores=cores, kind="port",
-                value_1thread=n * steps1 / el1, cpu_model=cpu_model(),
+                gbs=n * steps / el * bpp / 1e9, value_1thread=n * steps1 / el1,
+                gbs_1thread=n * steps1 / el1 * bpp / 1e9, cpu_model=cpu_model(),
                 sample=f"{n} params ({gdt} grads, {bits}-bit codes, B={B}) x {steps} steps, "
                        f"{el:.1f} s, oracle/mdq_oracle.c with {cores} OpenMP threads; "
                        f"1 thread: {steps1} steps, {el1:.1f} s")
