@@ -156,3 +156,26 @@ def test_optimizer_fused_transitions_match_separate_passes(cls, B):
             for k in ("exp_avg", "exp_avg_sq", "scale_m", "scale_v", "v_min"):
                 assert sa[k].dtype == sb[k].dtype and torch.equal(sa[k], sb[k]), (t, bits, i, k)
             assert torch.equal(a.detach(), b.detach()), (t, bits, i)
+
+
+@pytest.mark.parametrize("src,dst", [(2, 0), (0, 1), (1, 2), (3, 0)],
+                         ids=["s16-p4", "p4-s8", "s8-s16", "s32-p4"])
+def test_restore_with_nonfinite_grads_matches_separate_passes(src, dst):
+    """NaN and +-inf grads (the reference's NaN-skipping reductions, code 0 for a NaN quotient):
+    the storage-changing step still equals the separate passes bit for bit."""
+    B = 128
+    tag = f"restore {NAMES[src]} -> {NAMES[dst]} B={B} non-finite grads"
+    print(f"case: {tag}", flush=True)
+    a = Tensors(src, B, "f32", seed=77 + 10 * src + dst)
+    rng = np.random.default_rng(5)
+    for it in a.items:
+        g = it[1].clone()
+        n = g.numel()
+        idx = torch.from_numpy(rng.choice(n, size=max(1, n // 50), replace=False)).to(DEV)
+        vals = torch.tensor([float("nan"), float("inf"), float("-inf")], device=DEV)
+        g[idx] = vals[torch.arange(idx.numel(), device=DEV) % 3]
+        it[1] = g
+    b = a.clone()
+    separate_passes(a, dst, B, "nearest", 99, step=7)
+    fused(b, dst, B, "nearest", 99, step=7)
+    assert_same(a, b, tag)
