@@ -951,9 +951,10 @@ __global__ __launch_bounds__(Cfg<LOG2B>::THREADS) void mdq_step_kernel(const Mdq
 {
     using C = Cfg<LOG2B>;
     // Occupancy cap at 7 waves per SIMD: the clobber reserves v0..v71, so the
-    // register file never holds 8 of these waves.  With 8 (64 VGPRs or fewer)
-    // the LLaMA 4-bit step ran 1 % slower (same-allocation A/B 13.36 vs
-    // 13.23 ms): more requests in flight than the HBM streams profit from.
+    // register file never holds 8 of these waves, whatever the compiler's
+    // count.  With one contiguous eighth of the tiles per XCD, 8 waves ran the
+    // LLaMA 4-bit step 1 % slower (same-allocation A/B 13.36 vs 13.23 ms); with
+    // the chunked tile order below the two are level (+-0.3 %).
     asm volatile("" ::: "v71");
     constexpr bool USE_LUT = (SRC == ST_P4) && C::B >= 32;
     __shared__ float lut_s[USE_LUT ? C::TB * 16 : 1];
