@@ -256,22 +256,30 @@ int take_slot(DevCtx *ctx, size_t need, Slot **out)
 // itself would start only after the previous kernel there has finished, and
 // the next kernel would wait for it, leaving the GPU idle between
 // back-to-back steps.  The slot is free (take_slot waited for its last
-// launch), so the copy cannot overwrite descriptors still in use.  A stream
-// under graph capture gets the copy on itself.  Called with ctx->mu held.
-int upload(DevCtx *ctx, Slot &s, size_t bytes, hipStream_t stream)
+// launch), so the copy cannot overwrite descriptors still in use.  A launch
+// over fewer than SMALL_LAUNCH_ELEMS elements (a kernel of a few tens of
+// microseconds) gets the copy on `stream` itself: there the cross-stream wait
+// costs more than the overlap saves (flat 4M-element step 26.5 -> 17.7 us per
+// call; GPT-2 small, 124M elements, 277 us per call with the copy stream, 286
+// without; LLaMA-7B level).  So does a stream under graph capture.  Called
+// with ctx->mu held.
+constexpr int64_t SMALL_LAUNCH_ELEMS = int64_t(1) << 24;
+
+int upload(DevCtx *ctx, Slot &s, size_t bytes, int64_t elems, hipStream_t stream)
 {
     hipError_t e;
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     e = hipStreamIsCapturing(stream, &cs);
     if (e != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
-    if (cs == hipStreamCaptureStatusNone && !ctx->copy_stream) {
+    const bool on_stream = cs != hipStreamCaptureStatusNone || elems < SMALL_LAUNCH_ELEMS;
+    if (!on_stream && !ctx->copy_stream) {
         e = hipStreamCreateWithFlags(&ctx->copy_stream, hipStreamNonBlocking);
         if (e != hipSuccess) {
             ctx->copy_stream = nullptr;
             return hip_fail(e, "hipStreamCreate(descriptor copies)");
         }
     }
-    if (cs != hipStreamCaptureStatusNone) {
+    if (on_stream) {
         e = hipMemcpyAsync(s.dev, s.host, bytes, hipMemcpyHostToDevice, stream);
         return e == hipSuccess ? STQ_OK : hip_fail(e, "hipMemcpyAsync(descriptors)");
     }
@@ -312,7 +320,7 @@ int upload_and_launch(const std::vector<MdqDesc> &descs, int src_storage, int st
     std::memcpy(s.host, descs.data(), n * sizeof(MdqDesc));
     long long *tb = reinterpret_cast<long long *>(s.host + n * sizeof(MdqDesc));
     for (size_t i = 0; i < n; ++i) tb[i] = descs[i].tile_begin;
-    rc = upload(ctx, s, need, stream);
+    rc = upload(ctx, s, need, total_tiles * mdq::tile_elems(1 << log2b), stream);
     if (rc != STQ_OK) return rc;
     hipError_t e;
 
@@ -375,7 +383,7 @@ int run_grad_stats(const void *const *grads, const int64_t *numels, int n, int g
     std::memcpy(s->host, d.data(), (size_t)n * sizeof(mdq::StatDesc));
     long long *tb = reinterpret_cast<long long *>(s->host + (size_t)n * sizeof(mdq::StatDesc));
     for (int i = 0; i < n; ++i) tb[i] = d[i].tile_begin;
-    rc = upload(ctx, *s, up, stream);
+    rc = upload(ctx, *s, up, tiles * mdq::STAT_TILE, stream);
     if (rc != STQ_OK) return rc;
     hipError_t e;
     const mdq::StatDesc *dd = reinterpret_cast<const mdq::StatDesc *>(s->dev);
@@ -583,7 +591,7 @@ int run_convert(const stq_code_convert *items, int n, hipStream_t stream)
     std::memcpy(s->host, d.data(), m * sizeof(mdq::ConvDesc));
     long long *tb = reinterpret_cast<long long *>(s->host + m * sizeof(mdq::ConvDesc));
     for (size_t i = 0; i < m; ++i) tb[i] = d[i].tile_begin;
-    rc = upload(ctx, *s, need, stream);
+    rc = upload(ctx, *s, need, tiles * mdq::CONV_TILE, stream);
     if (rc != STQ_OK) return rc;
     hipError_t e;
     e = mdq::launch_convert(reinterpret_cast<const mdq::ConvDesc *>(s->dev),
