@@ -101,7 +101,15 @@ __global__ __launch_bounds__(ST_THREADS) void stats_partial_kernel(const StatDes
                                                                    double *__restrict__ partials)
 {
     __shared__ double lds[ST_WAVES][3];
-    const long long tile = blockIdx.x;
+    // Workgroup b runs on XCD x = b % 8 as its j-th (j = b / 8); the tiles go to
+    // the XCDs in round-robin chunks of 16 (2^19 elements), the workgroups of the
+    // last, partial round of 8 chunks take tile b (a bijection on [0, grid)).
+    // LLaMA-7B bf16 grads, same-allocation A/B: 1.89 ms against 2.00 ms for
+    // tile = b; chunks of 32-128 tiles run as 16.
+    constexpr unsigned CK = 16u;
+    const unsigned grid = gridDim.x, b = blockIdx.x, j = b >> 3, x = b & 7u;
+    const long long tile = b < grid / (8u * CK) * (8u * CK) ? (long long)((j / CK) * 8u + x) * CK + (j % CK)
+                                                            : (long long)b;
     // the tensor owning this tile: the last i with tile_begin[i] <= tile
     int lo = 0, hi = n - 1;
     while (lo < hi) {
