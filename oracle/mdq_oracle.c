@@ -207,6 +207,7 @@ int mdq_oracle_step(const mdqo_tensor *t, const mdqo_hparams *h)
     if (t->storage == MDQO_STORE_S8 && t->bits > 8) return -1;
     if (t->storage == MDQO_STORE_S16 && t->bits > 16) return -1;
     if (t->storage < 0 || t->storage > 3) return -1;
+    if (t->elem_offset < 0) return -1;
     if (n == 0) return 0;
     const int64_t nb = (n + B - 1) / B;
 
@@ -295,7 +296,7 @@ int mdq_oracle_step(const mdqo_tensor *t, const mdqo_hparams *h)
                 double qm, qv;
                 if (stochastic) {
                     float um, uv;
-                    sr_uniforms((uint64_t)idx, t->tensor_id, t->step, h->seed, &um, &uv);
+                    sr_uniforms((uint64_t)(idx + t->elem_offset), t->tensor_id, t->step, h->seed, &um, &uv);
                     qm = (double)floorf(fmaf(m, inv_dm, um));
                     qv = (double)floorf(fmaf(l - s_vmin, inv_dv, uv));
                 } else {

@@ -51,6 +51,8 @@ typedef struct {
     int32_t bits;          /* 1..32, within the storage width; 4 for P4         */
     int32_t step;          /* already incremented by the caller (>= 1)          */
     uint32_t tensor_id;    /* stochastic rounding stream id                     */
+    int64_t elem_offset;   /* index of element 0 in that stream (0: a whole     */
+                           /* tensor; a piece's start within its tensor)        */
 } mdqo_tensor;
 
 typedef struct {

@@ -24,7 +24,8 @@ v codes / scale_v      min-log element -> 0, max-log element -> 2^bits-1, tail l
                        force Lmax >= 0 (tests/test_oracle_step.py)
 AdamW update           bits=32: matches a float64 textbook AdamW with v0 = e^-20 to
                        1e-6; lr=0 leaves p; g=0 state=0 gives p*(1-lr*wd) exactly
-stochastic rounding    unbiasedness and code histogram (tests/test_oracle_step.py)
+stochastic rounding    unbiasedness and code histogram; pieces stepped with their element
+                       offsets reproduce the whole tensor (tests/test_oracle_step.py)
 NaN / inf grads        the reference's fmaxf / fminf reductions ignore NaN and its (int)
                        conversion maps NaN to 0: a NaN element leaves its block's scales
                        and other codes as a finite stand-in does, codes 0, p NaN; an inf
@@ -80,6 +81,7 @@ class _Tensor(ctypes.Structure):
         ("bits", ctypes.c_int32),
         ("step", ctypes.c_int32),
         ("tensor_id", ctypes.c_uint32),
+        ("elem_offset", ctypes.c_int64),
     ]
 
 
@@ -172,11 +174,13 @@ def step(p: np.ndarray, grad: np.ndarray, code_m: np.ndarray, code_v: Optional[n
          beta1: float, beta2: float, lr: float, weight_decay: float, eps: float,
          step: int, bits: int, block_size: int, storage: int,
          rounding: int = ROUND_NEAREST, seed: int = 0, tensor_id: int = 0,
-         threads: int = 0) -> None:
+         threads: int = 0, elem_offset: int = 0) -> None:
     """One fused step on numpy arrays, in place (p, codes, scales).
 
     ``grad`` may be float32, or a uint16 array holding bf16 (``grad_dtype``
-    inferred: float32 -> F32, uint16 -> BF16, float16 -> F16).
+    inferred: float32 -> F32, uint16 -> BF16, float16 -> F16).  ``elem_offset``:
+    the index of element 0 in the tensor's stochastic-rounding stream (a piece of
+    a larger tensor starting there draws that tensor's random numbers).
     """
     n = p.size
     assert p.dtype == np.float32
@@ -193,7 +197,7 @@ def step(p: np.ndarray, grad: np.ndarray, code_m: np.ndarray, code_v: Optional[n
     for s in (scale_m, scale_v, v_min):
         assert s.dtype == np.float32 and s.size >= nb
     t = _Tensor(_ptr(p), _ptr(grad), _ptr(code_m), _ptr(code_v), _ptr(scale_m), _ptr(scale_v),
-                _ptr(v_min), n, storage, gdt, block_size, bits, step, tensor_id)
+                _ptr(v_min), n, storage, gdt, block_size, bits, step, tensor_id, elem_offset)
     h = _HParams(beta1, beta2, lr, weight_decay, eps, rounding, seed, threads)
     rc = lib().mdq_oracle_step(ctypes.byref(t), ctypes.byref(h))
     if rc != 0:

@@ -249,3 +249,28 @@ def test_rejects_invalid(bad):
     with pytest.raises(ValueError):
         orc.step(np.zeros(n, np.float32), np.zeros(n, np.float32), st[0], st[1], st[2], st[3], st[4],
                  **HP, **args)
+
+
+@pytest.mark.parametrize("B,storage,bits", [(2, orc.STORE_S8, 8), (64, orc.STORE_P4, 4), (128, orc.STORE_S16, 16)])
+def test_pieces_with_elem_offset_reproduce_the_whole_tensor(B, storage, bits):
+    """Stochastic rounding of block-aligned pieces: a piece stepped with elem_offset = its start
+    draws the whole tensor's random numbers, so the pieces together give the whole tensor's step
+    bit for bit; with offset 0 they do not (each piece would restart the stream)."""
+    rng = np.random.default_rng(3)
+    n = 50 * B + 7
+    p0 = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    g = (rng.standard_normal(n) * 1e-3).astype(np.float32)
+    kw = dict(beta1=0.9, beta2=0.999, lr=1e-3, weight_decay=0.01, eps=1e-8, step=3, bits=bits, block_size=B,
+              storage=storage, rounding=orc.ROUND_STOCHASTIC, seed=5, tensor_id=9)
+    whole_p, whole = p0.copy(), list(orc.init_state(n, B, storage))
+    orc.step(whole_p, g, *whole, **kw)
+    cuts = [0, 13 * B, 31 * B, n]
+    for use_offset in (True, False):
+        pp, st = p0.copy(), list(orc.init_state(n, B, storage))
+        for s, e in zip(cuts[:-1], cuts[1:]):
+            b0, b1 = s // B, (e + B - 1) // B
+            orc.step(pp[s:e], g[s:e], st[0][s:e], None if st[1] is None else st[1][s:e],
+                     st[2][b0:b1], st[3][b0:b1], st[4][b0:b1], elem_offset=s if use_offset else 0, **kw)
+        same = np.array_equal(pp.view(np.uint32), whole_p.view(np.uint32)) and all(
+            np.array_equal(a, b) for a, b in zip(st, whole) if a is not None)
+        assert same == use_offset, use_offset
