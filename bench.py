@@ -478,7 +478,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the step shards by quant block across GPUs "
-              "with no communication inside the step; see DESIGN.md); run with --gpus 1", file=sys.stderr)
+              "with no communication inside the step; --shard-of N times one GPU's share); run with "
+              "--gpus 1", file=sys.stderr)
         sys.exit(2)
 
     import torch
