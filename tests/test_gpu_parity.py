@@ -342,3 +342,32 @@ def test_errors_follow_the_reference_messages():
         mdq_hip.fused_step(p, g, torch.full((256,), 8, dtype=torch.uint8, device=DEV),
                            torch.empty(0, dtype=torch.uint8, device=DEV), sm, sm.clone(), sm.clone(),
                            0.9, 0.999, 1e-3, 0.0, 1e-8, 1, 4, 128, torch.zeros(3, dtype=torch.int64, device=DEV))
+
+
+@pytest.mark.parametrize("storage,bits,B", [(orc.STORE_P4, 4, 64), (orc.STORE_P4, 4, 128), (orc.STORE_S8, 8, 128),
+                                            (orc.STORE_S8, 6, 256), (orc.STORE_S16, 12, 128)])
+def test_exact_and_near_ties_in_full_tiles(storage, bits, B):
+    """m on (k + 1/2) d exactly, one float ulp below and above it, for every k and both signs,
+    in whole one-wave tiles (the kernel's fast path): ties round away from zero, near-ties to
+    the nearest code, bit-exact against the oracle.  Fresh state and beta1 = 1/2 make m = g / 2
+    exact at step 1; each block's largest |m| = M sets d = (M + 1e-12) / 2^(bits-1) + 1e-12."""
+    print(f"case: ties storage={storage} bits={bits} B={B}", flush=True)
+    rng = np.random.default_rng(bits * 1000 + B)
+    n = 4 * 512
+    qm = 2 ** (bits - 1)
+    g = np.zeros(n, np.float32)
+    for blk in range(n // B):
+        M = np.float32(10.0 ** rng.uniform(-6, -2))
+        d = (M + np.float32(1e-12)) / np.float32(qm) + np.float32(1e-12)
+        ks = rng.integers(0, qm, B)
+        t = ((ks + 0.5) * np.float64(d)).astype(np.float32)
+        kind = rng.integers(0, 3, B)
+        t = np.where(kind == 1, np.nextafter(t, np.float32(0)), np.where(kind == 2, np.nextafter(t, np.float32(1)), t))
+        t = np.minimum(t, M) * np.where(rng.random(B) < 0.5, np.float32(-1), np.float32(1))
+        t[int(rng.integers(0, B))] = M * np.float32(1 if rng.random() < 0.5 else -1)
+        g[blk * B:(blk + 1) * B] = t * np.float32(2.0)
+    c = Case(n, B, storage, rng)
+    p_prev = c.p.copy()
+    c.oracle_step(g, 1, bits, beta1=0.5)
+    mdq_hip.multi_tensor_step([c.entry(to_dev(g), 1, bits, beta1=0.5)], B)
+    c.check(p_prev)
