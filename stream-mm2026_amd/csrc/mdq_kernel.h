@@ -597,15 +597,38 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
     // one fma for the v exponent and one for each moment.
     const float neg8sm = -8.0f * sm;
     float m[EPL], v[EPL], lv[EPL];
+    // Without the table every element takes an exp.  Its argument
+    // fma(c, sv, vmin) is non-decreasing in the code c when sv >= 0, so with
+    // c <= cmax (the storage's largest code) it lies in [vmin, fma(cmax, sv,
+    // vmin)]; when that interval is inside [-104, 89] for every lane of the
+    // wave, mdq_expf_core gives mdq_expf's bits without its clamps and selects.
+    bool core_exp = false;
+    if constexpr (!USE_LUT) {
+        constexpr float cmax = SRC == ST_P4 ? 15.0f : SRC == ST_S8 ? 255.0f : SRC == ST_S16 ? 65535.0f
+                                                                                           : 4294967296.0f;
+        const bool in = sv >= 0.0f && vmin >= -104.0f && fma_(cmax, sv, vmin) <= 89.0f;
+        core_exp = __builtin_amdgcn_ballot_w64(!in) == 0;
+    }
+    if (core_exp) {
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-        const float m0 = dequant_m<SRC>(mc[e], sm, neg8sm);
-        float v0;
-        if constexpr (USE_LUT) v0 = lut[bi * 16 + vc[e]];
-        else v0 = mdq_expf(fma_((float)vc[e], sv, vmin));
-        const float g = gv[e];
-        m[e] = fma_(d.b1, m0, d.omb1 * g);
-        v[e] = fma_(d.b2, v0, (d.omb2 * g) * g);
+        for (int e = 0; e < EPL; ++e) {
+            const float m0 = dequant_m<SRC>(mc[e], sm, neg8sm);
+            const float v0 = mdq_expf_core(fma_((float)vc[e], sv, vmin));
+            const float g = gv[e];
+            m[e] = fma_(d.b1, m0, d.omb1 * g);
+            v[e] = fma_(d.b2, v0, (d.omb2 * g) * g);
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+            const float m0 = dequant_m<SRC>(mc[e], sm, neg8sm);
+            float v0;
+            if constexpr (USE_LUT) v0 = lut[bi * 16 + vc[e]];
+            else v0 = mdq_expf(fma_((float)vc[e], sv, vmin));
+            const float g = gv[e];
+            m[e] = fma_(d.b1, m0, d.omb1 * g);
+            v[e] = fma_(d.b2, v0, (d.omb2 * g) * g);
+        }
     }
     if (prof_on) { unsigned long long t = clock64(); pa.c[1] += t - t0; t0 = t; }
 

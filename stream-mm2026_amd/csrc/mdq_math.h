@@ -41,18 +41,15 @@ MDQ_HD float floor_(float a) { return __builtin_floorf(a); }
 MDQ_HD float ldexp_(float a, int e) { return __builtin_ldexpf(a, e); }
 #endif
 
-// e^x.  NaN -> NaN, x > 89 -> +inf, x < -104 -> 0; in between the result is
-// 2^k * (1 + (r + r^2 E(r))) with a single rounding in the final scale.
-MDQ_HD float mdq_expf(float x)
+// The body of mdq_expf for xc in [-104, 89]: there the clamps and special-value
+// selects of mdq_expf leave xc and the result unchanged, so a caller that has
+// shown its arguments lie in that range may call this directly and gets the
+// same bits.
+MDQ_HD float mdq_expf_core(float xc)
 {
     const float log2e = bits_f(0x3fb8aa3bu);
     const float ln2_hi = bits_f(0x3f317218u);
     const float ln2_lo = bits_f(0xb102e308u);
-    // Clamp first so the integer conversion below is always in range; the
-    // special results are selected at the end.
-    float xc = x < -104.0f ? -104.0f : x;
-    xc = xc > 89.0f ? 89.0f : xc;
-    xc = (x == x) ? xc : 0.0f;
     float kf = rint_(xc * log2e);
     float r = fma_(-kf, ln2_hi, xc);
     r = fma_(-kf, ln2_lo, r);
@@ -65,7 +62,19 @@ MDQ_HD float mdq_expf(float x)
     float r2 = r * r;
     float t = fma_(r2, q, r);
     float e = 1.0f + t;
-    float res = ldexp_(e, (int)kf);
+    return ldexp_(e, (int)kf);
+}
+
+// e^x.  NaN -> NaN, x > 89 -> +inf, x < -104 -> 0; in between the result is
+// 2^k * (1 + (r + r^2 E(r))) with a single rounding in the final scale.
+MDQ_HD float mdq_expf(float x)
+{
+    // Clamp first so the integer conversion in the body is always in range;
+    // the special results are selected at the end.
+    float xc = x < -104.0f ? -104.0f : x;
+    xc = xc > 89.0f ? 89.0f : xc;
+    xc = (x == x) ? xc : 0.0f;
+    float res = mdq_expf_core(xc);
     res = x > 89.0f ? bits_f(0x7f800000u) : res;
     res = x < -104.0f ? 0.0f : res;
     return (x == x) ? res : x;
