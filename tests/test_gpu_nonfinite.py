@@ -100,3 +100,74 @@ def test_nonfinite_at_one_step_then_finite(storage, bits, B, rounding):
         mdq_hip.multi_tensor_step([c.entry(torch.from_numpy(g).to("cuda:0"), step, bits)], B,
                                   rounding="stochastic" if rounding else "nearest", seed=3)
         NonfiniteCase.check(c, p_prev)
+
+
+def _fma32(c, s, b):
+    """float32 fma(c, s, b) for |c| < 2^16: c * s and the sum are exact in float64."""
+    return np.float32(np.float64(c) * np.float64(s) + np.float64(b))
+
+
+def _top_scale(cmax, vmin, top):
+    """The largest float32 sv with fma(cmax, sv, vmin) <= top."""
+    s = np.float32((top - vmin) / cmax)
+    while _fma32(cmax, s, vmin) > top:
+        s = np.nextafter(s, np.float32(0))
+    while _fma32(cmax, np.nextafter(s, np.float32(np.inf)), vmin) <= top:
+        s = np.nextafter(s, np.float32(np.inf))
+    return s
+
+
+@pytest.mark.parametrize("storage,bits,B", [(orc.STORE_S8, 8, 128), (orc.STORE_S16, 16, 128), (orc.STORE_S8, 8, 64),
+                                            (orc.STORE_P4, 4, 16)])
+def test_exp_argument_range_edges(storage, bits, B):
+    """Steps without an exp table evaluate exp(code * sv + vmin) per element, and skip the exp's
+    clamps for a wave whose blocks all keep that argument inside [-104, 89].  Blocks at both ends
+    of that range (vmin = -104 exactly; the largest code landing on 88 or exactly 89) and blocks
+    just outside it or with negative, NaN or infinite scales, alone in a wave or beside in-range
+    blocks, all match the oracle over two steps."""
+    print(f"case: exp argument range edges storage={storage} bits={bits} B={B}", flush=True)
+    rng = np.random.default_rng(77 + bits + B)
+    lpw = {128: 4, 64: 8, 16: 32}[B]                     # quant blocks per one-wave tile
+    nw = 12
+    c = NonfiniteCase(B * lpw * nw, B, storage, rng)
+    cm, cv, sm, sv, vm = c.state
+    nb = sm.size
+    cmax = {orc.STORE_P4: 15, orc.STORE_S8: 255, orc.STORE_S16: 65535}[storage]
+    sm[:] = np.float32(1e-3)
+    vm[:] = np.float32(-20.0)
+    sv[:] = np.float32(0.05)
+    if storage == orc.STORE_P4:
+        cm[:] = rng.integers(0, 256, cm.size, dtype=np.uint8)
+        cm[0::B] &= 0x0F                                 # v code 0 at each block's first element
+        cm[B - 1::B] |= 0xF0                             # v code 15 at its last
+    else:
+        cm[:] = rng.integers(np.iinfo(cm.dtype).min, np.iinfo(cm.dtype).max + 1, cm.size, dtype=cm.dtype)
+        cv[:] = rng.integers(0, cmax + 1, cv.size, dtype=cv.dtype)
+        cv[0::B] = 0
+        cv[B - 1::B] = cmax
+    s88 = _top_scale(cmax, -104.0, 88.0)
+    v89 = np.float32(-104.0)                             # a v_min near -104 whose top lands on 89
+    while _fma32(cmax, _top_scale(cmax, v89, 89.0), v89) != np.float32(89.0):
+        v89 = np.nextafter(v89, np.float32(0))
+    s89 = _top_scale(cmax, v89, 89.0)
+    w = lambda k: slice(k * lpw, (k + 1) * lpw)          # the blocks of wave k
+    vm[w(0)], sv[w(0)] = -104.0, s88                     # in range, low end exactly -104
+    vm[w(1)], sv[w(1)] = v89, s89                        # in range, top exactly 89 (exp overflows)
+    vm[w(2)][1] = np.nextafter(np.float32(-104.0), np.float32(-np.inf))
+    vm[w(3)][2], sv[w(3)][2] = v89, np.nextafter(s89, np.float32(np.inf))      # top just above 89
+    sv[w(4)][0] = -0.01
+    sv[w(5)][1] = np.nan
+    vm[w(6)][2] = np.nan
+    sv[w(7)][3 % lpw] = np.inf
+    vm[w(8)][0], sv[w(8)][0] = -104.0, s88               # in range beside ordinary blocks
+    vm[w(9)][lpw - 1], sv[w(9)][lpw - 1] = -50.0, s88
+    for a, t in ((cm, c.tcm), (cv, c.tcv), (sm, c.tsm), (sv, c.tsv), (vm, c.tvm)):
+        if a is not None:
+            t.copy_(torch.from_numpy(a.copy()))
+    assert nb == lpw * nw
+    for step in (1, 2):
+        g, tg = Case.grads(c, rng)
+        p_prev = c.p.copy()
+        c.oracle_step(g, step, bits)
+        mdq_hip.multi_tensor_step([c.entry(tg, step, bits)], B)
+        c.check(p_prev)
