@@ -405,7 +405,7 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def cpu_baseline(gdt: str, bits: int, B: int, seconds: float):
+def cpu_baseline(gdt: str, bits: int, B: int, seconds: float, rounding: str = "nearest"):
     """The oracle (C, OpenMP over quant blocks) on a 2^24-param slice of the same
     workload, repeated for about `seconds` on this host's cores, then for a third of
     that on one thread; params/s."""
@@ -429,7 +429,8 @@ def cpu_baseline(gdt: str, bits: int, B: int, seconds: float):
         while True:
             done += 1
             orc.step(p, g, cm, cv, sm, sv, vm, beta1=0.9, beta2=0.999, lr=1e-3, weight_decay=0.01, eps=1e-8,
-                     step=done, bits=bits, block_size=B, storage=storage, threads=threads)
+                     step=done, bits=bits, block_size=B, storage=storage, threads=threads,
+                     rounding=orc.ROUND_STOCHASTIC if rounding == "stochastic" else orc.ROUND_NEAREST, seed=7)
             steps += 1
             el = time.perf_counter() - t0
             if el >= budget:
@@ -441,7 +442,7 @@ def cpu_baseline(gdt: str, bits: int, B: int, seconds: float):
     return dict(value=n * steps / el, unit="params/s", cores=cores, kind="port",
                 gbs=n * steps / el * bpp / 1e9, value_1thread=n * steps1 / el1,
                 gbs_1thread=n * steps1 / el1 * bpp / 1e9, cpu_model=cpu_model(),
-                sample=f"{n} params ({gdt} grads, {bits}-bit codes, B={B}) x {steps} steps, "
+                sample=f"{n} params ({gdt} grads, {bits}-bit codes, B={B}, {rounding}) x {steps} steps, "
                        f"{el:.1f} s, oracle/mdq_oracle.c with {cores} OpenMP threads; "
                        f"1 thread: {steps1} steps, {el1:.1f} s")
 
@@ -456,6 +457,8 @@ def main():
     ap.add_argument("--bits", type=int, default=None, choices=(4, 8, 16, 32),
                     help="code width (canonical storage: packed nibbles, int8/16/32 + uint8/16/32); "
                          "default: the config's (4)")
+    ap.add_argument("--rounding", default="nearest", choices=("nearest", "stochastic"),
+                    help="requant rounding of the timed launches (stochastic: Philox, seed 7)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--sweep-config5", action="store_true",
                     help="time BASELINE config 5 over bits x block x rounding (one JSON line with all points)")
@@ -504,13 +507,16 @@ def main():
         return
     w = build_workload(args.config, dev, bits=args.bits)
     plan = w["plan"]
+    if args.rounding == "stochastic":
+        import mdq_hip
+        plan = mdq_hip.MultiTensorPlan(w["entries"], w["B"], rounding="stochastic", seed=7)
     shard = None
     if args.shard_of > 1:
         import mdq_hip
         if not 0 <= args.shard_rank < args.shard_of:
             sys.exit(f"bench.py: --shard-rank must be in [0, {args.shard_of})")
         mine = mdq_hip.shard_states(w["entries"], w["B"], args.shard_of, args.shard_rank)
-        plan = mdq_hip.MultiTensorPlan(mine, w["B"])
+        plan = mdq_hip.MultiTensorPlan(mine, w["B"], rounding=args.rounding, seed=7)
         shard = dict(of=args.shard_of, rank=args.shard_rank, tensors=len(mine),
                      params=sum(e.p.numel() for e in mine))
         w["N"] = shard["params"]
@@ -570,7 +576,7 @@ def main():
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle) ...")
-        cpu = cpu_baseline(w["gdt"], w["bits"], w["B"], args.cpu_seconds)
+        cpu = cpu_baseline(w["gdt"], w["bits"], w["B"], args.cpu_seconds, args.rounding)
         log(f"cpu baseline: {cpu['value']:.3e} params/s on {cpu['cores']} cores, "
             f"{cpu['value_1thread']:.3e} on 1 thread ({cpu['cpu_model']})")
 
@@ -596,11 +602,12 @@ def main():
                          f"{shard['tensors']} tensors): ") +
                         f"{N} fp32 params, {w['gdt']} grads, "
                         f"{w['bits']}-bit {'packed ' if w['bits'] == 4 else ''}m/v codes, block {w['B']}, "
-                        f"nearest rounding, one multi-tensor launch",
+                        f"{args.rounding} rounding, one multi-tensor launch",
             "params": N,
             "tensors": w["tensors"],
             "block_size": w["B"],
             "bits": w["bits"],
+            "rounding": args.rounding,
             "grad_dtype": w["gdt"],
             "bytes_per_param": bpp,
         },

@@ -562,6 +562,25 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
             }
         }
     }
+    // The Philox words of stochastic rounding depend only on the element
+    // indices, the step and the seed: drawn here, while the loads above are in
+    // flight, their integer work overlaps the memory latency.  Counter
+    // (quad index lo, hi, tensor id, step), key = seed; word i serves element
+    // 4q+i.  Element indices count from rng_origin (a multiple of B, so of 4
+    // wherever a lane owns whole quads).
+    uint32_t rw[SR && C::QPL > 0 ? EPL : 1];
+    if constexpr (SR && C::QPL > 0) {
+#pragma unroll
+        for (int k = 0; k < C::QPL; ++k) {
+            const uint64_t q = (uint64_t)(((base + d.rng_origin) >> 2) + lane_quad<PAIRED, LOG2B>(j, k));
+            const U4 r = mdq_philox4x32_10_uk(U4{(uint32_t)q, (uint32_t)(q >> 32), d.tensor_id, d.step},
+                                              (uint32_t)seed, (uint32_t)(seed >> 32));
+            rw[4 * k + 0] = r.x;
+            rw[4 * k + 1] = r.y;
+            rw[4 * k + 2] = r.z;
+            rw[4 * k + 3] = r.w;
+        }
+    }
     if constexpr (narrows_codes<SRC, DST>()) {
         constexpr float lo = DST == ST_S16 ? -32768.0f : -128.0f;
         constexpr float hi = DST == ST_S16 ? 32767.0f : 127.0f;
@@ -752,24 +771,17 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
             // wherever a lane owns whole quads).
             if constexpr (C::QPL > 0) {
 #pragma unroll
-                for (int k = 0; k < C::QPL; ++k) {
-                    const uint64_t q = (uint64_t)(((base + d.rng_origin) >> 2) + lane_quad<PAIRED, LOG2B>(j, k));
-                    U4 r = mdq_philox4x32_10(U4{(uint32_t)q, (uint32_t)(q >> 32), d.tensor_id, d.step},
-                                             (uint32_t)seed, (uint32_t)(seed >> 32));
-                    const uint32_t w[4] = {r.x, r.y, r.z, r.w};
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        um[4 * k + i] = mdq_u16_uniform(w[i] & 0xffffu);
-                        uv[4 * k + i] = mdq_u16_uniform(w[i] >> 16);
-                    }
+                for (int e = 0; e < EPL; ++e) {
+                    um[e] = mdq_u16_uniform(rw[e] & 0xffffu);
+                    uv[e] = mdq_u16_uniform(rw[e] >> 16);
                 }
             } else {
 #pragma unroll
                 for (int e = 0; e < EPL; ++e) {
                     const uint64_t idx = (uint64_t)(base + d.rng_origin + e);
                     const uint64_t q = idx >> 2;
-                    U4 r = mdq_philox4x32_10(U4{(uint32_t)q, (uint32_t)(q >> 32), d.tensor_id, d.step},
-                                             (uint32_t)seed, (uint32_t)(seed >> 32));
+                    U4 r = mdq_philox4x32_10_uk(U4{(uint32_t)q, (uint32_t)(q >> 32), d.tensor_id, d.step},
+                                                (uint32_t)seed, (uint32_t)(seed >> 32));
                     const uint32_t w[4] = {r.x, r.y, r.z, r.w};
                     const uint32_t ww = w[idx & 3];
                     um[e] = mdq_u16_uniform(ww & 0xffffu);

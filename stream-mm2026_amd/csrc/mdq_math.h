@@ -182,6 +182,45 @@ MDQ_HD U4 mdq_philox4x32_10(U4 c, uint32_t k0, uint32_t k1)
     return c;
 }
 
+#if defined(__HIPCC__)
+// a ^ b ^ k as one v_bitop3_b32 (truth table 0x96, the three-input XOR), which
+// the compiler does not form by itself.  k is passed in a scalar register, so
+// it must be wave-uniform.
+__device__ __forceinline__ uint32_t xor3_uk(uint32_t a, uint32_t b, uint32_t k)
+{
+#if defined(__HIP_DEVICE_COMPILE__)
+    uint32_t r;
+    asm("v_bitop3_b32 %0, %1, %2, %3 bitop3:0x96" : "=v"(r) : "v"(a), "v"(b), "s"(k));
+    return r;
+#else
+    return a ^ b ^ k;
+#endif
+}
+
+// mdq_philox4x32_10 for a wave-uniform key (the step kernel's seed), same
+// result.  Round 0 keeps the plain XORs (its tensor-id and step words are
+// uniform too, so the compiler folds them in scalar registers); the other nine
+// rounds fuse each output word's two XORs.
+__device__ __forceinline__ U4 mdq_philox4x32_10_uk(U4 c, uint32_t k0, uint32_t k1)
+{
+    {
+        const uint64_t p0 = (uint64_t)0xD2511F53u * c.x;
+        const uint64_t p1 = (uint64_t)0xCD9E8D57u * c.z;
+        c = U4{(uint32_t)(p1 >> 32) ^ c.y ^ k0, (uint32_t)p1, (uint32_t)(p0 >> 32) ^ c.w ^ k1, (uint32_t)p0};
+    }
+#pragma unroll
+    for (int r = 1; r < 10; ++r) {
+        k0 += 0x9E3779B9u;
+        k1 += 0xBB67AE85u;
+        const uint64_t p0 = (uint64_t)0xD2511F53u * c.x;
+        const uint64_t p1 = (uint64_t)0xCD9E8D57u * c.z;
+        c = U4{xor3_uk((uint32_t)(p1 >> 32), c.y, k0), (uint32_t)p1, xor3_uk((uint32_t)(p0 >> 32), c.w, k1),
+               (uint32_t)p0};
+    }
+    return c;
+}
+#endif
+
 // Uniforms on the centred 2^-16 grid: (k + 1/2) / 65536, k in [0, 65535].
 MDQ_HD float mdq_u16_uniform(uint32_t k16) { return ((float)k16 + 0.5f) * (1.0f / 65536.0f); }
 
