@@ -14,8 +14,10 @@ from typing import Optional, Sequence
 import numpy as np
 import torch
 
-from . import _capi
+from . import _capi, storage
 from ._capi import ROUND_NEAREST, ROUND_STOCHASTIC, StqTensor, check, dtype_code, lib
+from .storage import STORE_P4, STORE_S8, STORE_S16, STORE_S32, empty_codes
+from .storage import layout_of as storage_of
 
 __all__ = [
     "ROUND_NEAREST", "ROUND_STOCHASTIC", "STORE_P4", "STORE_S8", "STORE_S16", "STORE_S32",
@@ -24,7 +26,7 @@ __all__ = [
     "block_aligned_ranges", "shard_states",
     "device_math", "device_math_digests", "device_log_approx_error", "host_math", "host_round_half_away",
     "host_div_code_range", "host_philox",
-    "lib", "rounding_code",
+    "lib", "rounding_code", "storage",
 ]
 
 
@@ -186,6 +188,21 @@ class MultiTensorPlan:
                 return False
             ptrs.append(g.data_ptr())
         self.arr["grad"] = ptrs
+        return True
+
+    def try_set_params(self, params: Sequence[torch.Tensor]) -> bool:
+        """Refresh the param pointers (``p.data`` may have been replaced by a tensor elsewhere,
+        as ``Module.to()`` does); False (nothing changed) when a param no longer fits its row:
+        another dtype, size or device, or not contiguous."""
+        if len(params) != self.n:
+            return False
+        di = self._dev_index
+        ptrs = []
+        for p, n in zip(params, self._numel):
+            if p.dtype is not torch.float32 or p.get_device() != di or p.numel() != n or not p.is_contiguous():
+                return False
+            ptrs.append(p.data_ptr())
+        self.arr["p"] = ptrs
         return True
 
     def set_hparams(self, lr=None, beta1=None, beta2=None, eps=None, weight_decay=None, bits=None) -> None:
@@ -368,33 +385,9 @@ def grad_stats(grads: Sequence[torch.Tensor], out: Optional[torch.Tensor] = None
     return out
 
 
-STORE_P4, STORE_S8, STORE_S16, STORE_S32 = 0, 1, 2, 3
-_STORE_DTYPES = {STORE_S8: (torch.int8, torch.uint8), STORE_S16: (torch.int16, torch.uint16),
-                 STORE_S32: (torch.int32, torch.uint32)}
 # stq_code_convert: 4 pointers, int64 numel, two int32 storages (48 bytes)
 STQ_CONVERT_DTYPE = np.dtype([("src_m", np.uint64), ("src_v", np.uint64), ("dst_m", np.uint64),
                               ("dst_v", np.uint64), ("numel", np.int64), ("src", np.int32), ("dst", np.int32)])
-
-
-def storage_of(exp_avg: torch.Tensor, exp_avg_sq: torch.Tensor) -> int:
-    """The code storage class of a state's (exp_avg, exp_avg_sq) pair."""
-    if exp_avg.dtype == torch.uint8 and exp_avg_sq.numel() == 0:
-        return STORE_P4
-    for st, (dm, dv) in _STORE_DTYPES.items():
-        if exp_avg.dtype == dm and exp_avg_sq.dtype == dv and exp_avg_sq.numel() == exp_avg.numel():
-            return st
-    raise RuntimeError(f"no code storage class for exp_avg {exp_avg.dtype} / exp_avg_sq {exp_avg_sq.dtype}"
-                       f"[{exp_avg_sq.numel()}]")
-
-
-def empty_codes(like: torch.Tensor, storage: int):
-    """Uninitialised (exp_avg, exp_avg_sq) of ``like``'s shape and device in ``storage``."""
-    if storage == STORE_P4:
-        return (torch.empty_like(like, dtype=torch.uint8, memory_format=torch.contiguous_format),
-                torch.empty(0, dtype=torch.uint8, device=like.device))
-    dm, dv = _STORE_DTYPES[storage]
-    return (torch.empty_like(like, dtype=dm, memory_format=torch.contiguous_format),
-            torch.empty_like(like, dtype=dv, memory_format=torch.contiguous_format))
 
 
 def convert_codes(items) -> None:

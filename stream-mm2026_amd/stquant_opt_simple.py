@@ -1,34 +1,44 @@
 """MDQAdamWSimple -- drop-in for /root/reference/CUDA/stquant_opt_simple.py on MI355X.
 
-Same constructor, param groups, ``step()``, state layout (per param: ``step``,
-``exp_avg`` / ``exp_avg_sq`` integer codes -- packed nibbles in ``exp_avg`` and an
-empty ``exp_avg_sq`` at 4 bits --, ``scale_m``, ``scale_v``, ``v_min`` per quant
-block, ``current_bit``, ``last_score``), ``state_dict`` extras, bit-distribution
-getters and timing keys as the reference.
+Kept from the reference, because callers and checkpoints depend on it:
+- the constructor and param groups, ``step()``;
+- the per-param state: ``step``, the ``exp_avg`` / ``exp_avg_sq`` integer codes (packed
+  nibbles and an empty ``exp_avg_sq`` at 4 bits), ``scale_m``, ``scale_v``, ``v_min`` per quant
+  block, ``current_bit``, ``last_score``;
+- the ``state_dict`` extras, the bit-distribution getters and the timing keys.
 
-What differs is underneath: instead of one kernel launch per tensor bracketed by
-two device synchronisations (:242-265), ``step()`` runs ONE multi-tensor HIP
-launch per storage class through the C ABI of ``libstquant_hip.so``
-(``mdq_hip.multi_tensor_step``).  Tensors whose bit width changed go through
-one launch of the storage-changing step (``mdq_hip.multi_tensor_restore``: the
-reference's align -> kernel -> pack of :140-280 in one pass, block sizes
-64 / 128 / 256), or else through device conversions with exactly the
-reference's storage rules (:140-210).  Results per element are those of the
-reference kernel (:246-263 -> stquant_kernel.cu).
+The machinery underneath is different:
+- ``step()`` makes one multi-tensor HIP launch per bucket of tensors, through the C ABI of
+  ``libstquant_hip.so`` (``mdq_hip.MultiTensorPlan``). The reference launches once per tensor,
+  with a device synchronisation on either side (:242-265).
+- Launch plans are cached. A step over the same tensors as the last one only refreshes
+  pointers, steps and hyper-parameters (the steady path).
+- A tensor whose bit width changed has its codes moved to the new layout (``mdq_hip.storage``)
+  inside the step kernel: ``mdq_hip.multi_tensor_restore`` reads the old layout and writes the
+  new one in one pass. Block sizes other than 64 / 128 / 256 get one conversion launch before
+  the step and one after.
+- The MDQ bit decision takes its gradient statistics from one fused launch
+  (``mdq_hip.grad_stats``) and reads all scores back to the host once.
 
-New optional param-group keys (defaults keep the reference behaviour):
-``bits`` (fixed code width 4/8/16/32 instead of the score-based choice; such groups still
-count in the global gradient statistics that score the other groups),
-``rounding`` ('nearest' or 'stochastic') and ``seed`` (stochastic stream).
-``sync_timing=False`` skips the device synchronisations that fill the timing
-dict (and the kernel phase profile), so ``step()`` issues its work
-asynchronously on the current stream.
+Results per element are those of the reference kernel (:246-263 -> stquant_kernel.cu).
+
+New optional param-group keys (the defaults keep the reference's behaviour):
+- ``bits``: a fixed code width 4/8/16/32 instead of the score-based choice. Tensors in such
+  groups still count in the global gradient statistics that score the other groups.
+- ``rounding``: 'nearest' or 'stochastic'.
+- ``seed``: the seed of the stochastic-rounding stream.
+
+New constructor options:
+- ``sync_timing=False`` skips the device synchronisations that fill the timing dict and the
+  kernel phase profile, so ``step()`` issues its work asynchronously on the current stream.
+- ``grad_stats='reference'`` computes the bit decision's statistics with the reference's per-tensor
+  torch reductions instead of the fused launch.
 """
 from __future__ import annotations
 
 import math
 import time
-from collections import OrderedDict
+from collections import Counter, OrderedDict
 
 import numpy as np
 import torch
@@ -36,6 +46,69 @@ import torch.distributed as dist
 from torch.optim import Optimizer
 
 import mdq_hip
+from mdq_hip import storage as codes
+
+# Timing-dict keys of the reference (stquant_opt_simple.py:392-405, :486-493, :282-316).
+_PHASE_KEYS = ("mdq_kernel_dequant_ms", "mdq_kernel_adam_mv_ms", "mdq_kernel_scale_reduce_ms",
+               "mdq_kernel_quant_ms", "mdq_kernel_update_p_ms")
+_DECISION_KEYS = ("mdq_stats_ms", "mdq_bit_decision_ms", "mdq_grad_stats_ms", "mdq_allreduce_ms",
+                  "mdq_score_bits_ms")
+_KERNEL_WALL_KEYS = ("quant_dequant_unpack_ms", "quant_dequant_kernel_ms", "quant_dequant_pack_ms")
+# score thresholds of the widths above 4 bits, widest first (stquant_opt_simple.py:100-109)
+_WIDTH_THRESHOLDS = ((32, 24.0), (16, 12.0), (8, 6.8))
+_REPORTED_WIDTHS = (4, 8, 16, 32)
+
+
+class _PhaseProfile:
+    """The kernel's five phase cycle sums (dequant, moments, scale reduction, requant, param
+    update) in an int64 device buffer, and their split of a measured kernel wall time
+    (the reference's ``profile_cycles``, stquant_opt_simple.py:56-83)."""
+
+    SLOTS = len(_PHASE_KEYS)
+
+    def __init__(self):
+        self.buf = None
+
+    def on(self, device) -> torch.Tensor:
+        if self.buf is None or self.buf.device != device:
+            self.buf = torch.zeros(self.SLOTS, dtype=torch.int64, device=device)
+        return self.buf
+
+    def active(self, device):
+        """The buffer if it lives on ``device``, else None (profiling off)."""
+        buf = self.buf
+        return buf if buf is not None and buf.device == device else None
+
+    def cycles(self, device):
+        return self.on(device).double().cpu().tolist()
+
+    def split(self, device, wall_ms: float):
+        """``wall_ms`` shared out in proportion to the phases' cycles."""
+        if wall_ms <= 0:
+            return [0.0] * self.SLOTS
+        cyc = self.cycles(device)
+        total = sum(cyc)
+        return [wall_ms * (c / total) for c in cyc] if total > 0 else [0.0] * self.SLOTS
+
+
+class _Stopwatch:
+    """Milliseconds between entry and exit, with a device synchronisation at both ends when
+    ``sync`` is set (the reference brackets every timed phase that way)."""
+
+    def __init__(self, device, sync: bool = True):
+        self.device, self.sync, self.ms = device, sync, 0.0
+
+    def __enter__(self):
+        if self.sync and self.device.type == "cuda":
+            torch.cuda.synchronize(self.device)
+        self._t = time.perf_counter()
+        return self
+
+    def __exit__(self, *exc):
+        if exc[0] is None and self.sync and self.device.type == "cuda":
+            torch.cuda.synchronize(self.device)
+        self.ms = (time.perf_counter() - self._t) * 1000.0
+        return False
 
 
 class MDQAdamWSimple(Optimizer):
@@ -57,88 +130,47 @@ class MDQAdamWSimple(Optimizer):
         sync_timing=True,
         grad_stats="fused",
     ):
-        # stquant_opt_simple.py:33-44
-        tau_adaptive = 300 * math.log(layer_count) * math.sqrt(batch_size)
-        if bits is not None and int(bits) not in (4, 8, 16, 32):
+        if bits is not None and int(bits) not in _REPORTED_WIDTHS:
             raise ValueError(f"bits must be one of 4, 8, 16, 32 or None, got {bits}")
         mdq_hip.rounding_code(rounding)
         if grad_stats not in ("fused", "reference"):
             raise ValueError(f"grad_stats must be 'fused' or 'reference', got {grad_stats!r}")
-        defaults = dict(
-            lr=lr,
-            betas=betas,
-            eps=eps,
-            weight_decay=weight_decay,
-            alpha=alpha,
-            tau=tau_adaptive,
-            update_freq=update_freq,
-            block_size=block_size,
-            bits=bits,
-            rounding=rounding,
-            seed=seed,
-        )
-        super().__init__(params, defaults)
-
-        self.n_ema = None
-        self.r_ema = None
-        self.v_global_ema = None
+        # the schedule's time constant, stquant_opt_simple.py:33
+        tau = 300 * math.log(layer_count) * math.sqrt(batch_size)
+        super().__init__(params, dict(lr=lr, betas=betas, eps=eps, weight_decay=weight_decay, alpha=alpha,
+                                      tau=tau, update_freq=update_freq, block_size=block_size, bits=bits,
+                                      rounding=rounding, seed=seed))
+        # global EMAs of the bit decision (0-d tensors once the first decision ran)
+        self.n_ema = self.r_ema = self.v_global_ema = None
         self.total_steps = 0
         self.last_step_timings = {}
         self.sync_timing = sync_timing
         self.grad_stats = grad_stats
-        self._kernel_profile_buf = None
-        self._kernel_profile_device = None
+        self._profile = _PhaseProfile()
 
-    _KERNEL_PROF_SLOTS = 5
     # launch-plan class of ``_run_kernels`` (a test harness substitutes its own executor)
     _plan_cls = mdq_hip.MultiTensorPlan
-    # storage changes of CUDA tensors in one conversion launch per step; False keeps the
-    # reference's per-tensor torch passes (same results)
+    # False: layout changes of CUDA tensors run as torch ops per tensor instead of device launches
     _device_transitions = True
-    # with device transitions: a tensor whose storage changes is stepped by a kernel that reads
-    # the old storage and writes the new one (block sizes 64 / 128 / 256), instead of convert ->
-    # step -> pack; False keeps the separate passes (same results)
+    # False: a layout change always takes the separate convert -> step -> convert launches,
+    # even where the storage-changing step kernel exists (block sizes 64 / 128 / 256)
     _fused_transitions = True
+    _RESTORE_GRAD_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
 
     def add_param_group(self, param_group):
         self.__dict__["_steady"] = None
         super().add_param_group(param_group)
 
-    # ------------------------------------------------------------------
-    # kernel phase profile (stquant_opt_simple.py:56-83)
-    # ------------------------------------------------------------------
-    def _kernel_profile_buf_for(self, device):
-        if self._kernel_profile_buf is None or self._kernel_profile_device != device:
-            self._kernel_profile_buf = torch.zeros(self._KERNEL_PROF_SLOTS, dtype=torch.int64, device=device)
-            self._kernel_profile_device = device
-        return self._kernel_profile_buf
-
-    def _reset_kernel_profile(self, device):
-        self._kernel_profile_buf_for(device).zero_()
-
-    def _read_kernel_profile_cycles(self, device):
-        buf = self._kernel_profile_buf_for(device)
-        return buf.double().cpu().tolist()
-
-    def _kernel_phases_ms_from_wall(self, device, kernel_wall_ms):
-        if kernel_wall_ms <= 0:
-            return [0.0] * self._KERNEL_PROF_SLOTS
-        cycles = self._read_kernel_profile_cycles(device)
-        total = sum(cycles)
-        if total <= 0:
-            return [0.0] * self._KERNEL_PROF_SLOTS
-        return [kernel_wall_ms * (c / total) for c in cycles]
-
-    @staticmethod
-    def _sync_device(device):
-        if device.type == "cuda":
-            torch.cuda.synchronize(device)
+    def get_last_step_timings(self):
+        return dict(self.last_step_timings)
 
     # ------------------------------------------------------------------
-    # grad stats and bit choice (stquant_opt_simple.py:93-109)
+    # bit decision (stquant_opt_simple.py:93-109, :407-482)
     # ------------------------------------------------------------------
     @staticmethod
     def _compute_grad_stats(grad: torch.Tensor) -> torch.Tensor:
+        # the reference's fp32 torch expression (stquant_opt_simple.py:93-98); its op order fixes
+        # the statistics' rounding and so the widths chosen near a threshold
         n_l = torch.sqrt(torch.mean(grad * grad))
         r_l = torch.std(grad) / (grad.abs().mean() + 1e-12)
         v_l = torch.mean(grad * grad)
@@ -167,321 +199,161 @@ class MDQAdamWSimple(Optimizer):
 
     @staticmethod
     def _score_to_bits(score) -> int:
+        """The widest width whose threshold the score reaches; 4 bits otherwise (NaN too)."""
         s = float(score.item()) if torch.is_tensor(score) and score.numel() == 1 else float(score)
-        if s >= 24:
-            return 32
-        if s >= 12:
-            return 16
-        if s >= 6.8:
-            return 8
-        return 4
+        return next((bits for bits, lo in _WIDTH_THRESHOLDS if s >= lo), 4)
+
+    def _fold_ema(self, mean: torch.Tensor) -> None:
+        """Fold this decision's mean statistics ``[n, r, v]`` into the global EMAs (the first
+        decision assigns them); the same fp32 ops per component as the reference's :433-440."""
+        if self.n_ema is None:
+            self.n_ema, self.r_ema, self.v_global_ema = mean.unbind(0)
+            return
+        a = self.param_groups[0]["alpha"]
+        prev = torch.stack((self.n_ema, self.r_ema, self.v_global_ema))
+        self.n_ema, self.r_ema, self.v_global_ema = (a * mean + (1 - a) * prev).unbind(0)
+
+    def _decide_bits(self, work) -> None:
+        """Score every tensor with a grad against the global statistics and give the tensors of
+        scored groups their width; fills the decision's timing keys."""
+        dev = work[0][0].device
+        lt = self.last_step_timings
+        with _Stopwatch(dev) as sw:
+            stats = self._all_grad_stats([p.grad for p, _g in work])
+        lt["mdq_grad_stats_ms"] = sw.ms
+        mean = stats.mean(dim=0)
+        if dist.is_available() and dist.is_initialized():
+            with _Stopwatch(dev) as sw:
+                dist.all_reduce(mean, op=dist.ReduceOp.SUM)
+                mean /= dist.get_world_size()
+            lt["mdq_allreduce_ms"] = sw.ms
+        with _Stopwatch(dev) as sw:
+            self._fold_ema(mean)
+            states = [self.state[p] for p, _g in work]
+            scores = self._scores(stats, [st["step"] for st in states], self.param_groups[0]["tau"])
+            host = scores.cpu().tolist()                 # the step's one device -> host read
+            for (_p, g), st, s, h in zip(work, states, scores.unbind(0), host):
+                st["last_score"] = s
+                if g.get("bits") is None:
+                    st["current_bit"] = self._score_to_bits(h)
+        lt["mdq_score_bits_ms"] = sw.ms
 
     # ------------------------------------------------------------------
-    # code storage pack / unpack / align (stquant_opt_simple.py:114-210)
+    # state
     # ------------------------------------------------------------------
     @staticmethod
-    def _is_momentum_packed4(state):
-        if "exp_avg" not in state or "exp_avg_sq" not in state:
-            return False
-        ea, easq = state["exp_avg"], state["exp_avg_sq"]
-        return ea.dtype == torch.uint8 and easq.numel() == 0 and ea.numel() > 0
+    def _fresh_state(p, block: int):
+        """A tensor's state before its first step (stquant_opt_simple.py:212-225): 16-bit zero
+        codes, zero scales and v_min = -20 per quant block, so v starts at e^-20 (quirk Q1)."""
+        m, v = codes.zero_codes(p, codes.STORE_S16)
+        nblk = -(-p.numel() // block)
+        return {"step": 0, "exp_avg": m, "exp_avg_sq": v,
+                "scale_m": torch.zeros(nblk, dtype=torch.float32, device=p.device),
+                "scale_v": torch.zeros(nblk, dtype=torch.float32, device=p.device),
+                "v_min": torch.full((nblk,), -20.0, dtype=torch.float32, device=p.device),
+                "current_bit": 16, "last_score": torch.tensor(12.0, device=p.device)}
+
+    @staticmethod
+    def _layout(state) -> int:
+        return codes.layout_of(state["exp_avg"], state["exp_avg_sq"])
 
     @classmethod
     def _storage_matches_bits(cls, state, bits: int) -> bool:
-        """True when the code storage is already the one ``bits`` uses
-        (stquant_opt_fused_io.py:19-37); aligning and re-packing are no-ops then."""
+        """True when the codes already rest in the layout a ``bits``-wide step leaves, so the
+        step needs no layout change (stquant_opt_fused_io.py:19-37).  As there, an empty tensor
+        never counts as packed."""
         if "exp_avg" not in state:
             return False
-        ea, easq = state["exp_avg"], state.get("exp_avg_sq")
-        if bits == 4:
-            return cls._is_momentum_packed4(state)
-        if bits == 8:
-            return (
-                ea.dtype == torch.int8
-                and easq is not None
-                and easq.dtype == torch.uint8
-                and easq.numel() == ea.numel()
-            )
-        if bits == 16:
-            return ea.dtype == torch.int16 and easq is not None and easq.dtype == torch.uint16
-        if bits >= 32:
-            return ea.dtype == torch.int32 and easq is not None and easq.dtype == torch.uint32
-        return False
-
-    @staticmethod
-    def _unpack_packed4_momentum(state):
-        packed = state["exp_avg"]
-        m_u = (packed.to(torch.int32) & 0x0F).to(torch.int16)
-        v_q = ((packed.to(torch.int32) >> 4) & 0x0F).to(torch.int32)
-        state["exp_avg"] = (m_u - 8).to(torch.int8)
-        state["exp_avg_sq"] = v_q.to(torch.uint8)
-
-    @staticmethod
-    def _pack_momentum_to_nibbles(state):
-        ea, easq = state["exp_avg"], state["exp_avg_sq"]
-        if ea.dtype != torch.int8 or easq.numel() != ea.numel():
-            return
-        dev = ea.device
-        m_u = (ea.to(torch.int16) + 8).clamp(0, 15).to(torch.uint8)
-        v_lo = easq.to(torch.int32).clamp(0, 15).to(torch.uint8)
-        state["exp_avg"] = (m_u | (v_lo << 4)).to(dev)
-        state["exp_avg_sq"] = torch.empty(0, dtype=torch.uint8, device=dev)
-
-    @classmethod
-    def _align_momentum_storage(cls, state, bits):
-        if cls._is_momentum_packed4(state):
-            cls._unpack_packed4_momentum(state)
-
-        ea, easq = state["exp_avg"], state["exp_avg_sq"]
-
-        if bits >= 32:
-            if ea.dtype != torch.int32:
-                state["exp_avg"] = ea.to(torch.int32)
-            if easq.dtype != torch.uint32:
-                state["exp_avg_sq"] = easq.to(torch.uint32)
-            return
-
-        if bits > 8:
-            if ea.dtype == torch.int8:
-                state["exp_avg"] = ea.to(torch.int16)
-                state["exp_avg_sq"] = easq.to(torch.uint16)
-            elif ea.dtype == torch.int32:
-                state["exp_avg"] = ea.clamp(-32768, 32767).to(torch.int16)
-                state["exp_avg_sq"] = easq.to(torch.int64).clamp(0, 65535).to(torch.uint16)
-            elif ea.dtype != torch.int16:
-                state["exp_avg"] = ea.to(torch.int16)
-                state["exp_avg_sq"] = easq.to(torch.uint16)
-            return
-
-        if ea.dtype == torch.int16:
-            state["exp_avg"] = ea.clamp(-128, 127).to(torch.int8)
-            state["exp_avg_sq"] = easq.to(torch.int64).clamp(0, 255).to(torch.uint8)
-        elif ea.dtype == torch.int32:
-            state["exp_avg"] = ea.clamp(-128, 127).to(torch.int8)
-            state["exp_avg_sq"] = easq.to(torch.int64).clamp(0, 255).to(torch.uint8)
-        elif ea.dtype == torch.int8 and easq.numel() > 0 and easq.dtype != torch.uint8:
-            state["exp_avg_sq"] = easq.to(torch.uint8)
-
-    @classmethod
-    def _pack_momentum_storage(cls, state, bits):
-        ea, easq = state["exp_avg"], state["exp_avg_sq"]
-
-        if bits <= 8:
-            if ea.dtype == torch.int16:
-                state["exp_avg"] = ea.clamp(-128, 127).to(torch.int8)
-                state["exp_avg_sq"] = easq.to(torch.int64).clamp(0, 255).to(torch.uint8)
-            elif ea.dtype == torch.int32:
-                state["exp_avg"] = ea.clamp(-128, 127).to(torch.int8)
-                state["exp_avg_sq"] = easq.to(torch.int64).clamp(0, 255).to(torch.uint8)
-            elif ea.dtype == torch.int8 and easq.numel() > 0 and easq.dtype != torch.uint8:
-                state["exp_avg_sq"] = easq.to(torch.uint8)
-
-            if (
-                bits == 4
-                and state["exp_avg"].dtype == torch.int8
-                and state["exp_avg_sq"].numel() == state["exp_avg"].numel()
-            ):
-                cls._pack_momentum_to_nibbles(state)
-            return
-
-        if bits == 16:
-            if ea.dtype == torch.int32:
-                state["exp_avg"] = ea.clamp(-32768, 32767).to(torch.int16)
-                state["exp_avg_sq"] = easq.to(torch.int64).clamp(0, 65535).to(torch.uint16)
-            elif ea.dtype == torch.int8:
-                state["exp_avg"] = ea.to(torch.int16)
-                state["exp_avg_sq"] = easq.to(torch.uint16)
-            return
-
-        if bits >= 32:
-            if ea.dtype != torch.int32:
-                state["exp_avg"] = ea.to(torch.int32)
-            if easq.dtype != torch.uint32:
-                state["exp_avg_sq"] = easq.to(torch.uint32)
-
-    def _init_state_if_needed(self, p, state, block_size):
-        # stquant_opt_simple.py:212-225
-        if len(state) != 0:
-            return
-        state["step"] = 0
-        state["exp_avg"] = torch.zeros_like(p, dtype=torch.int16, memory_format=torch.contiguous_format)
-        state["exp_avg_sq"] = torch.zeros_like(p, dtype=torch.uint16, memory_format=torch.contiguous_format)
-        num_blocks = (p.numel() + block_size - 1) // block_size
-        state["scale_m"] = torch.zeros(num_blocks, dtype=torch.float32, device=p.device)
-        state["scale_v"] = torch.zeros(num_blocks, dtype=torch.float32, device=p.device)
-        state["v_min"] = torch.full((num_blocks,), -20.0, dtype=torch.float32, device=p.device)
-        state["current_bit"] = 16
-        state["last_score"] = torch.tensor(12.0, device=p.device)
-
-    def get_last_step_timings(self):
-        return dict(self.last_step_timings)
-
-    # ------------------------------------------------------------------
-    # per-tensor preparation around the batched kernel
-    # ------------------------------------------------------------------
-    def _prepare_update(self, p, group):
-        """Per-tensor work before the kernel: ``step += 1`` and the storage
-        alignment of stquant_opt_simple.py:231-239.  Returns True when the
-        storage must be re-packed after the kernel (:269).
-
-        A state whose storage already fits ``bits`` is handed to the kernel
-        as it is: for packed nibbles at 4 bits, unpack -> int8/uint8 kernel ->
-        re-pack (the reference's route) yields the same codes, scales and params
-        byte for byte; for the other widths aligning and packing change nothing.
-        """
-        state = self.state[p]
-        bits = int(state["current_bit"])
-        state["step"] += 1
-        if self._storage_matches_bits(state, bits):
+        rest = codes.resting_layout(bits)
+        try:
+            lay = cls._layout(state)
+        except RuntimeError:
             return False
-        pending = self.__dict__.get("_pending_align")
-        if pending is not None and state["exp_avg"].is_cuda:
-            pending.append((p, group, state, bits))    # one launch for all (_flush_align)
-        else:
-            self._align_momentum_storage(state, bits)
-        return True
+        return lay == rest and not (rest == codes.STORE_P4 and state["exp_avg"].numel() == 0)
 
-    def _finish_update(self, p):
+    def _begin_update(self, p, group) -> bool:
+        """``step += 1`` for the tensor; True when its codes must change layout this step."""
         state = self.state[p]
-        bits = int(state["current_bit"])
-        pending = self.__dict__.get("_pending_pack")
-        if pending is not None and state["exp_avg"].is_cuda:
-            pending.append((state, bits))
-        else:
-            self._pack_momentum_storage(state, bits)
+        state["step"] += 1
+        return not self._storage_matches_bits(state, int(state["current_bit"]))
 
-    @staticmethod
-    def _aligned_storage(bits: int) -> int:
-        """The code storage _align_momentum_storage leaves for ``bits`` (:166-198)."""
-        if bits >= 32:
-            return mdq_hip.STORE_S32
-        if bits > 8:
-            return mdq_hip.STORE_S16
-        return mdq_hip.STORE_S8
-
-    @classmethod
-    def _final_storage(cls, bits: int):
-        """The code storage a step at ``bits`` leaves (align, kernel, pack: :140-219), or None
-        for widths the storage cannot hold (17..31 bits go to int16 there)."""
-        if bits == 4:
-            return mdq_hip.STORE_P4
-        if 1 <= bits <= 16 or bits == 32:
-            return cls._aligned_storage(bits)
-        return None
-
-    _RESTORE_GRAD_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
-
-    @staticmethod
-    def _convert_states(moves):
-        """Re-store the codes of ``[(state, dst_storage)]`` with one conversion launch."""
-        items, news = [], []
-        for state, dst in moves:
+    # ------------------------------------------------------------------
+    # layout changes
+    # ------------------------------------------------------------------
+    def _move_codes(self, moves) -> None:
+        """Re-store the codes of ``[(state, layout)]``: one device launch for the CUDA tensors
+        (``_device_transitions``), the torch value map for the rest."""
+        launch, news = [], []
+        for state, kind in moves:
             ea, easq = state["exp_avg"], state["exp_avg_sq"]
-            nm, nv = mdq_hip.empty_codes(ea, dst)
-            items.append((ea, easq, nm, nv))
+            if ea.is_cuda and self._device_transitions and ea.numel() > 0:
+                nm, nv = codes.empty_codes(ea, kind)
+                launch.append((ea, easq, nm, nv))
+            else:
+                nm, nv = codes.restore(ea, easq, kind)
             news.append((state, nm, nv))
-        mdq_hip.convert_codes(items)
+        if launch:
+            mdq_hip.convert_codes(launch)
         for state, nm, nv in news:
             state["exp_avg"], state["exp_avg_sq"] = nm, nv
 
-    def _flush_align(self):
-        """Device version of _align_momentum_storage for all deferred tensors: the same value map
-        (unpack nibbles, widen, or clamp to the narrower range; :140-198) in one launch.
-
-        Tensors that a storage-changing kernel can step (``_fused_transitions``) are not
-        converted: they get destination codes in their final storage and are collected in
-        ``self._restores`` for ``_run_restores``."""
-        pending, self._pending_align = self.__dict__.get("_pending_align") or [], None
-        moves = []
-        restores = {}
-        for p, group, state, bits in pending:
-            if state["exp_avg"].numel() == 0:          # the reference's dtype rules for empty tensors
-                self._align_momentum_storage(state, bits)
-                continue
-            src = mdq_hip.storage_of(state["exp_avg"], state["exp_avg_sq"])
-            fin = self._final_storage(bits)
-            if (self._fused_transitions and fin is not None and fin != src
+    def _split_moves(self, moved):
+        """Of the tensors whose layout changes: ``{id(p): (p, group, state, new codes)}`` for
+        the storage-changing step kernel, and ``[(p, group)]`` for separate conversions."""
+        fused, separate = {}, []
+        for p, group in moved:
+            state = self.state[p]
+            rest = codes.resting_layout(int(state["current_bit"]))
+            ea = state["exp_avg"]
+            if (self._fused_transitions and self._device_transitions and ea.is_cuda and ea.numel() > 0
+                    and rest is not None and rest != self._layout(state)
                     and min(int(group["block_size"]), 1024) in mdq_hip.RESTORE_BLOCK_SIZES
                     and p.grad.dtype in self._RESTORE_GRAD_DTYPES):
-                restores[id(p)] = (p, group, state, mdq_hip.empty_codes(state["exp_avg"], fin))
-                continue
-            dst = self._aligned_storage(bits)
-            if src != dst:
-                moves.append((state, dst))
-        if moves:
-            self._convert_states(moves)
-        self._restores = restores
+                fused[id(p)] = (p, group, state, codes.empty_codes(ea, rest))
+            else:
+                separate.append((p, group))
+        return fused, separate
 
-    def _run_restores(self, restores):
-        """Storage-changing steps: one launch per (device, source storage, destination storage,
-        grad dtype, block size, rounding, seed), then the new codes replace the old ones."""
-        buckets = OrderedDict()
+    def _entries(self, rows):
+        """``mdq_hip.TensorState`` of ``[(p, group, state, grad)]``."""
         ids = self._tensor_ids
+        return [mdq_hip.TensorState(
+            p=p, grad=gr, exp_avg=st["exp_avg"], exp_avg_sq=st["exp_avg_sq"], scale_m=st["scale_m"],
+            scale_v=st["scale_v"], v_min=st["v_min"], step=st["step"], bits=int(st["current_bit"]),
+            lr=g["lr"], beta1=g["betas"][0], beta2=g["betas"][1], eps=g["eps"],
+            weight_decay=g["weight_decay"], tensor_id=ids.get(p, 0)) for p, g, st, gr in rows]
+
+    def _run_restores(self, restores) -> None:
+        """Storage-changing steps: one launch per (device, source layout, destination layout,
+        grad dtype, block size, rounding, seed); the new codes then replace the old ones."""
+        buckets = OrderedDict()
         for p, group, state, out in restores:
             grad = p.grad if p.grad.is_contiguous() else p.grad.contiguous()
-            key = (p.device, mdq_hip.storage_of(state["exp_avg"], state["exp_avg_sq"]),
-                   mdq_hip.storage_of(*out), grad.dtype, min(int(group["block_size"]), 1024),
-                   mdq_hip.rounding_code(group.get("rounding", "nearest")), int(group.get("seed", 0) or 0))
+            key = (p.device, self._layout(state), codes.layout_of(*out), grad.dtype,
+                   min(int(group["block_size"]), 1024), mdq_hip.rounding_code(group.get("rounding", "nearest")),
+                   int(group.get("seed", 0) or 0))
             buckets.setdefault(key, []).append((p, group, state, out, grad))
-        for key, lst in buckets.items():
-            dev, bsz, rnd, seed = key[0], key[4], key[5], key[6]
-            entries = [mdq_hip.TensorState(
-                p=p, grad=gr, exp_avg=st["exp_avg"], exp_avg_sq=st["exp_avg_sq"], scale_m=st["scale_m"],
-                scale_v=st["scale_v"], v_min=st["v_min"], step=st["step"], bits=int(st["current_bit"]),
-                lr=g["lr"], beta1=g["betas"][0], beta2=g["betas"][1], eps=g["eps"],
-                weight_decay=g["weight_decay"], tensor_id=ids.get(p, 0)) for p, g, st, _o, gr in lst]
-            prof = None
-            if self.sync_timing and self._kernel_profile_buf is not None and self._kernel_profile_device == dev:
-                prof = self._kernel_profile_buf
-            mdq_hip.multi_tensor_restore(entries, [o for _p, _g, _st, o, _gr in lst], bsz, rounding=rnd,
+        for (dev, _src, _dst, _gdt, block, rnd, seed), rows in buckets.items():
+            entries = self._entries([(p, g, st, gr) for p, g, st, _o, gr in rows])
+            prof = self._profile.active(dev) if self.sync_timing else None
+            mdq_hip.multi_tensor_restore(entries, [o for _p, _g, _st, o, _gr in rows], block, rounding=rnd,
                                          seed=seed, profile_cycles=prof)
-            for _p, _g, st, (nm, nv), _gr in lst:
+            for _p, _g, st, (nm, nv), _gr in rows:
                 st["exp_avg"], st["exp_avg_sq"] = nm, nv
 
-    def _flush_pack(self):
-        """Device version of _pack_momentum_storage after the step: 4-bit tensors in int8/uint8
-        storage go to nibbles (:214-219) in one launch; after alignment every other width
-        is already in its final storage."""
-        pending, self._pending_pack = self.__dict__.get("_pending_pack") or [], None
-        moves = []
-        for state, bits in pending:
-            if (bits == 4 and state["exp_avg"].numel() > 0
-                    and mdq_hip.storage_of(state["exp_avg"], state["exp_avg_sq"]) == mdq_hip.STORE_S8):
-                moves.append((state, mdq_hip.STORE_P4))
-            else:
-                self._pack_momentum_storage(state, bits)
-        if moves:
-            self._convert_states(moves)
-
-    def _launch_fused_update(self, p, group):
-        """Single-tensor update with the reference's per-tensor timing (:231-280)."""
-        t0 = time.perf_counter()
-        repack = self._prepare_update(p, group)
-        unpack_ms = (time.perf_counter() - t0) * 1000.0
-        self._sync_device(p.device)
-        tk0 = time.perf_counter()
-        self._run_kernels([(p, group)])
-        self._sync_device(p.device)
-        kernel_ms = (time.perf_counter() - tk0) * 1000.0
-        t1 = time.perf_counter()
-        if repack:
-            self._finish_update(p)
-        pack_ms = (time.perf_counter() - t1) * 1000.0
-        lt = self.last_step_timings
-        lt["quant_dequant_unpack_ms"] = lt.get("quant_dequant_unpack_ms", 0.0) + unpack_ms
-        lt["quant_dequant_kernel_ms"] = lt.get("quant_dequant_kernel_ms", 0.0) + kernel_ms
-        lt["quant_dequant_pack_ms"] = lt.get("quant_dequant_pack_ms", 0.0) + pack_ms
-
+    # ------------------------------------------------------------------
+    # the multi-tensor launches
+    # ------------------------------------------------------------------
     def _run_kernels(self, items):
         """Group tensors by (device, code storage, grad dtype, block size,
         rounding, seed) and run one multi-tensor launch per group; returns
         ``[(plan, indices into items), ...]``.
 
-        Each group's launch plan is cached and reused while its tensors and
-        their state tensors stay the same objects (bit-width transitions replace
-        state tensors and so rebuild the plan); per step only the grad
-        pointers, steps, bit widths and hyper-parameters are refreshed.  Plans
-        keep no reference to gradients.
+        Each group's launch plan is cached and reused while its params and
+        their state tensors are the same objects at the same addresses (a layout
+        change replaces state tensors, ``p.data = ...`` moves a param; both
+        rebuild the plan); per step only the grad pointers, steps, bit widths and
+        hyper-parameters are refreshed.  Plans keep no reference to gradients.
         """
         buckets = OrderedDict()
         for i, (p, group) in enumerate(items):
@@ -497,42 +369,32 @@ class MDQAdamWSimple(Optimizer):
                    int(group.get("seed", 0) or 0))
             buckets.setdefault(key, []).append((p, group, state, grad, i))
         cache = self.__dict__.setdefault("_plan_cache", {})
-        ids = self._tensor_ids
         runs = []
-        for key, lst in buckets.items():
-            lst = [x[:4] for x in lst]
-            idx = [x[4] for x in buckets[key]]
-            dev, bsz, rnd, seed = key[0], key[5], key[6], key[7]
-            sig = tuple((id(p), id(st["exp_avg"]), id(st["exp_avg_sq"]), id(st["scale_m"]),
-                         id(st["scale_v"]), id(st["v_min"])) for p, _g, st, _gr in lst)
+        for key, rows in buckets.items():
+            idx = [r[4] for r in rows]
+            rows = [r[:4] for r in rows]
+            dev, block, rnd, seed = key[0], key[5], key[6], key[7]
+            sig = tuple((id(p), p.data_ptr()) + tuple((id(st[k]), st[k].data_ptr()) for k in _STATE_TENSORS)
+                        for p, _g, st, _gr in rows)
             plan = cache.get(key)
             if plan is None or plan.sig != sig:
-                entries = [mdq_hip.TensorState(
-                    p=p, grad=gr, exp_avg=st["exp_avg"], exp_avg_sq=st["exp_avg_sq"], scale_m=st["scale_m"],
-                    scale_v=st["scale_v"], v_min=st["v_min"], step=st["step"], bits=int(st["current_bit"]),
-                    lr=g["lr"], beta1=g["betas"][0], beta2=g["betas"][1], eps=g["eps"],
-                    weight_decay=g["weight_decay"], tensor_id=ids.get(p, 0)) for p, g, st, gr in lst]
-                plan = self._plan_cls(entries, bsz, rounding=rnd, seed=seed)
+                plan = self._plan_cls(self._entries(rows), block, rounding=rnd, seed=seed)
                 plan.entries = None          # no references to grads
                 # Strong references to the params and state tensors the plan points
                 # at: while they are held no other object can reuse their id(), so
                 # the id signature identifies exactly these tensors.
-                plan.keep = [(p, st["exp_avg"], st["exp_avg_sq"], st["scale_m"], st["scale_v"], st["v_min"])
-                             for p, _g, st, _gr in lst]
+                plan.keep = [(p,) + tuple(st[k] for k in _STATE_TENSORS) for p, _g, st, _gr in rows]
                 plan.sig = sig
                 cache[key] = plan
             else:
-                plan.set_grads([gr for _p, _g, _st, gr in lst])
-                plan.set_steps([st["step"] for _p, _g, st, _gr in lst])
+                plan.set_grads([gr for _p, _g, _st, gr in rows])
+                plan.set_steps([st["step"] for _p, _g, st, _gr in rows])
                 plan.set_hparams(
-                    lr=[g["lr"] for _p, g, _st, _gr in lst], beta1=[g["betas"][0] for _p, g, _st, _gr in lst],
-                    beta2=[g["betas"][1] for _p, g, _st, _gr in lst], eps=[g["eps"] for _p, g, _st, _gr in lst],
-                    weight_decay=[g["weight_decay"] for _p, g, _st, _gr in lst],
-                    bits=[int(st["current_bit"]) for _p, _g, st, _gr in lst])
-            prof = None
-            if self.sync_timing and self._kernel_profile_buf is not None and self._kernel_profile_device == dev:
-                prof = self._kernel_profile_buf
-            plan.run(prof)
+                    lr=[g["lr"] for _p, g, _st, _gr in rows], beta1=[g["betas"][0] for _p, g, _st, _gr in rows],
+                    beta2=[g["betas"][1] for _p, g, _st, _gr in rows], eps=[g["eps"] for _p, g, _st, _gr in rows],
+                    weight_decay=[g["weight_decay"] for _p, g, _st, _gr in rows],
+                    bits=[int(st["current_bit"]) for _p, _g, st, _gr in rows])
+            plan.run(self._profile.active(dev) if self.sync_timing else None)
             runs.append((plan, idx))
         # plans of buckets that no longer exist keep pointers to dropped tensors
         for key in [k for k in cache if k not in buckets]:
@@ -541,321 +403,218 @@ class MDQAdamWSimple(Optimizer):
 
     @property
     def _tensor_ids(self):
+        """Position of each param over all groups: the tensor id of its stochastic-rounding stream."""
         ids = getattr(self, "_tensor_id_cache", None)
         if ids is None or len(ids) != sum(len(g["params"]) for g in self.param_groups):
-            ids = {}
-            k = 0
-            for g in self.param_groups:
-                for p in g["params"]:
-                    ids[p] = k
-                    k += 1
+            ids = {p: k for k, p in enumerate(p for g in self.param_groups for p in g["params"])}
             self._tensor_id_cache = ids
         return ids
 
-    def _finalize_step_timings(self, profile_device):
-        # stquant_opt_simple.py:282-316
-        unpack = self.last_step_timings.get("quant_dequant_unpack_ms", 0.0)
-        pack = self.last_step_timings.get("quant_dequant_pack_ms", 0.0)
-        kernel_wall = self.last_step_timings.get("quant_dequant_kernel_ms", 0.0)
+    def _batched_update(self, work):
+        """One step of every tensor in ``work``:
+        - tensors whose codes already rest in their width's layout go straight to the step
+          launches;
+        - tensors whose layout changes take the storage-changing step kernel where it exists,
+          else a conversion to the kernel layout before the step and one to the resting layout
+          after it.
 
-        self.last_step_timings["mdq_unpack_ms"] = unpack
-        self.last_step_timings["mdq_pack_ms"] = pack
-        self.last_step_timings["mdq_fused_kernel_ms"] = kernel_wall
-        self.last_step_timings["mdq_quant_dequant_ms"] = unpack + kernel_wall + pack
-
-        if profile_device is not None:
-            k_ms = self._kernel_phases_ms_from_wall(profile_device, kernel_wall)
-            (
-                self.last_step_timings["mdq_kernel_dequant_ms"],
-                self.last_step_timings["mdq_kernel_adam_mv_ms"],
-                self.last_step_timings["mdq_kernel_scale_reduce_ms"],
-                self.last_step_timings["mdq_kernel_quant_ms"],
-                self.last_step_timings["mdq_kernel_update_p_ms"],
-            ) = k_ms
-            self.last_step_timings["mdq_kernel_phases_sum_ms"] = sum(k_ms)
-            self.last_step_timings["mdq_kernel_profile_cycles"] = self._read_kernel_profile_cycles(profile_device)
-        else:
-            for key in (
-                "mdq_kernel_dequant_ms",
-                "mdq_kernel_adam_mv_ms",
-                "mdq_kernel_scale_reduce_ms",
-                "mdq_kernel_quant_ms",
-                "mdq_kernel_update_p_ms",
-                "mdq_kernel_phases_sum_ms",
-                "mdq_kernel_profile_cycles",
-            ):
-                self.last_step_timings[key] = 0.0 if key != "mdq_kernel_profile_cycles" else []
-
-    # ------------------------------------------------------------------
-    # metrics / checkpoint (stquant_opt_simple.py:321-378)
-    # ------------------------------------------------------------------
-    def get_bit_distribution(self):
-        counts = {4: 0, 8: 0, 16: 0, 32: 0}
-        num_tensors = 0
-        for group in self.param_groups:
-            for p in group["params"]:
-                st = self.state.get(p)
-                if st and "current_bit" in st:
-                    b = int(st["current_bit"])
-                    counts[b] = counts.get(b, 0) + 1
-                    num_tensors += 1
-        if num_tensors == 0:
-            return {4: 0.0, 8: 0.0, 16: 0.0, 32: 0.0}
-        return {b: (c / num_tensors) * 100.0 for b, c in counts.items()}
-
-    def get_bit_distribution_param_weighted(self):
-        counts_numel = {4: 0, 8: 0, 16: 0, 32: 0}
-        for group in self.param_groups:
-            for p in group["params"]:
-                st = self.state.get(p)
-                if st and "current_bit" in st:
-                    b = int(st["current_bit"])
-                    counts_numel[b] = counts_numel.get(b, 0) + p.numel()
-        total = sum(counts_numel.values())
-        if total == 0:
-            return {4: 0.0, 8: 0.0, 16: 0.0, 32: 0.0}
-        return {k: (v / total) * 100.0 for k, v in counts_numel.items()}
-
-    def get_avg_bit_param_weighted(self):
-        dist_bits = self.get_bit_distribution_param_weighted()
-        return float(sum(b * (perc / 100.0) for b, perc in dist_bits.items()))
-
-    def get_all_raw_scores(self):
-        scores = []
-        for group in self.param_groups:
-            for p in group["params"]:
-                st = self.state.get(p)
-                if st and "last_score" in st:
-                    scores.append(float(st["last_score"].item()))
-        return scores
-
-    def state_dict(self):
-        out = super().state_dict()
-        out["mdq_global_stats"] = {
-            "n_ema": self.n_ema,
-            "r_ema": self.r_ema,
-            "v_global_ema": self.v_global_ema,
-            "total_steps": self.total_steps,
-        }
-        return out
-
-    _CODE_KEYS = ("exp_avg", "exp_avg_sq")
-
-    def load_state_dict(self, state_dict):
-        """As stquant_opt_simple.py:371-378, plus the repair the reference lacks:
-        torch's ``Optimizer.load_state_dict`` casts every floating-point-param
-        state tensor to the param dtype, turning integer codes into float32.
-        The code values are small integers (exact in float32); each code tensor
-        is cast back to the integer dtype it had in ``state_dict``.  torch also
-        moves per-param state to the param's device, but not the global EMA
-        statistics; they are moved to the device of the first param (where the
-        bit decision computes them), so a checkpoint written on one device
-        resumes on another."""
-        self._steady = None
-        self.__dict__.pop("_plan_cache", None)
-        saved_dtypes = {}
-        for pid, st in state_dict.get("state", {}).items():
-            saved_dtypes[pid] = {k: st[k].dtype for k in self._CODE_KEYS
-                                 if k in st and torch.is_tensor(st[k])}
-        state_dict = dict(state_dict)
-        if "mdq_global_stats" in state_dict:
-            stats = state_dict.pop("mdq_global_stats")
-            self.n_ema = stats["n_ema"]
-            self.r_ema = stats["r_ema"]
-            self.v_global_ema = stats["v_global_ema"]
-            self.total_steps = stats["total_steps"]
-        super().load_state_dict(state_dict)
-        params = [p for g in self.param_groups for p in g["params"]]
-        saved_ids = [pid for g in state_dict["param_groups"] for pid in g["params"]]
-        for pid, p in zip(saved_ids, params):
-            st = self.state.get(p)
-            if not st:
-                continue
-            for k, dt in saved_dtypes.get(pid, {}).items():
-                if st[k].dtype != dt:
-                    st[k] = st[k].to(dt)
-        if params:
-            for k in ("n_ema", "r_ema", "v_global_ema"):
-                v = getattr(self, k)
-                if torch.is_tensor(v) and v.device != params[0].device:
-                    setattr(self, k, v.to(params[0].device))
+        The timing keys are filled as the reference's per-tensor loop fills them (:501-502).
+        """
+        dev = work[0][0].device
+        lt = self.last_step_timings
+        t0 = time.perf_counter()
+        flags = [self._begin_update(p, g) for p, g in work]
+        moved = [w for w, f in zip(work, flags) if f]
+        fused, separate = self._split_moves(moved)
+        self._move_codes([(self.state[p], codes.kernel_layout(int(self.state[p]["current_bit"])))
+                          for p, _g in separate])
+        unpack_ms = (time.perf_counter() - t0) * 1000.0
+        with _Stopwatch(dev, self.sync_timing) as sw:
+            direct = [w for w in work if id(w[0]) not in fused]
+            runs = self._run_kernels(direct) if direct else []
+            if fused:
+                self._run_restores(list(fused.values()))
+        t1 = time.perf_counter()
+        packs = []
+        for p, _g in separate:
+            st = self.state[p]
+            rest = codes.resting_layout(int(st["current_bit"]))
+            if rest is not None and rest != self._layout(st):
+                packs.append((st, rest))
+        self._move_codes(packs)
+        pack_ms = (time.perf_counter() - t1) * 1000.0
+        lt["quant_dequant_unpack_ms"] += unpack_ms
+        lt["quant_dequant_kernel_ms"] += sw.ms
+        lt["quant_dequant_pack_ms"] += pack_ms
+        # No storage was replaced: the plans just launched describe the state as
+        # it stands, so the next step can reuse them (``_steady_step``).
+        self._steady = self._make_steady(work, runs) if runs and not moved else None
 
     # ------------------------------------------------------------------
     # step (stquant_opt_simple.py:383-508)
     # ------------------------------------------------------------------
+    def _new_timings(self, decide: bool, update_freq) -> dict:
+        lt = dict.fromkeys(_DECISION_KEYS, 0.0)
+        lt.update(mdq_update_decision=decide, mdq_update_freq=update_freq)
+        lt.update(dict.fromkeys(_KERNEL_WALL_KEYS, 0.0))
+        lt.update(mdq_fused_io_fast_path_params=0, mdq_fused_io_fallback_params=0)
+        return lt
+
+    def _finalize_step_timings(self, profile_device):
+        """Derived timing keys of the reference (:282-316): totals of the three kernel-side walls,
+        and the kernel wall split into its five phases by their cycle shares (zeros and an empty
+        cycle list when the params are not on a GPU)."""
+        lt = self.last_step_timings
+        unpack, kernel, pack = (lt.get(k, 0.0) for k in _KERNEL_WALL_KEYS)
+        lt.update(mdq_unpack_ms=unpack, mdq_pack_ms=pack, mdq_fused_kernel_ms=kernel,
+                  mdq_quant_dequant_ms=unpack + kernel + pack)
+        if profile_device is None:
+            lt.update(dict.fromkeys(_PHASE_KEYS, 0.0), mdq_kernel_phases_sum_ms=0.0, mdq_kernel_profile_cycles=[])
+            return
+        phases = self._profile.split(profile_device, kernel)
+        lt.update(zip(_PHASE_KEYS, phases))
+        lt["mdq_kernel_phases_sum_ms"] = sum(phases)
+        lt["mdq_kernel_profile_cycles"] = self._profile.cycles(profile_device)
+
+    def _profile_device(self, device):
+        """The device whose phase profile this step fills (buffer zeroed), or None."""
+        if not self.sync_timing or device.type != "cuda":
+            return None
+        self._profile.on(device).zero_()
+        return device
+
     @torch.no_grad()
     def step(self, closure=None):
         loss = None
         if closure is not None:
             with torch.enable_grad():
                 loss = closure()
-
         self.total_steps += 1
-        self.last_step_timings = {
-            "mdq_stats_ms": 0.0,
-            "mdq_bit_decision_ms": 0.0,
-            "mdq_grad_stats_ms": 0.0,
-            "mdq_allreduce_ms": 0.0,
-            "mdq_score_bits_ms": 0.0,
-            "mdq_update_decision": False,
-            "mdq_update_freq": 0,
-            "quant_dequant_unpack_ms": 0.0,
-            "quant_dequant_kernel_ms": 0.0,
-            "quant_dequant_pack_ms": 0.0,
-            "mdq_fused_io_fast_path_params": 0,
-            "mdq_fused_io_fallback_params": 0,
-        }
-
         update_freq = self.param_groups[0]["update_freq"]
-        update_decision = (self.total_steps % update_freq == 0) or (self.total_steps < 5)
-        self.last_step_timings["mdq_update_decision"] = update_decision
-        self.last_step_timings["mdq_update_freq"] = update_freq
+        # steps 1-4 and every update_freq-th step re-decide the widths (:407)
+        decide = self.total_steps < 5 or self.total_steps % update_freq == 0
+        self.last_step_timings = self._new_timings(decide, update_freq)
 
-        sc = self._steady_lookup(update_decision)
+        sc = self._steady_lookup(decide)
         if sc is not None:
-            for key in ("mdq_grad_stats_ms", "mdq_allreduce_ms", "mdq_score_bits_ms", "mdq_stats_ms",
-                        "mdq_bit_decision_ms", "mdq_extra_stats_ms"):
-                self.last_step_timings[key] = 0.0
-            dev = sc["params"][0].device
-            profile_device = dev if self.sync_timing and dev.type == "cuda" else None
-            if profile_device is not None:
-                self._reset_kernel_profile(profile_device)
+            self.last_step_timings["mdq_extra_stats_ms"] = 0.0
+            prof_dev = self._profile_device(sc["params"][0].device)
             if self._steady_step(sc):
-                self._finalize_step_timings(profile_device)
+                self._finalize_step_timings(prof_dev)
                 return loss
         self._steady = None
 
-        params_with_grad = []
-
+        work = []
         for group in self.param_groups:
-            b_size = min(int(group.get("block_size", 256)), 1024)
+            block = min(int(group.get("block_size", 256)), 1024)
             for p in group["params"]:
                 if p.grad is None:
                     continue
-                params_with_grad.append((p, group))
-                state = self.state[p]
-                self._init_state_if_needed(p, state, b_size)
-
-        # Fixed-width groups (new ``bits`` option) take their width; tensors of the other groups
-        # are scored against global statistics over every tensor with a grad, as the reference
-        # computes them (it has no fixed groups).
-        for p, group in params_with_grad:
+                work.append((p, group))
+                if not self.state[p]:
+                    self.state[p].update(self._fresh_state(p, block))
+        # Fixed-width groups take their width; the other groups' tensors are scored against
+        # global statistics over every tensor with a grad, as the reference computes them (it
+        # has no fixed groups).
+        for p, group in work:
             if group.get("bits") is not None:
                 self.state[p]["current_bit"] = int(group["bits"])
-        scored = any(g.get("bits") is None for _p, g in params_with_grad)
-
-        grad_stats_ms = 0.0
-        allreduce_ms = 0.0
-        score_bits_ms = 0.0
-
-        stats_tensor = None
-        if update_decision and params_with_grad and scored:
-            dev = params_with_grad[0][0].device
-            self._sync_device(dev)
-            t_grad = time.perf_counter()
-            stats_tensor = self._all_grad_stats([p.grad for p, _g in params_with_grad])
-            self._sync_device(dev)
-            grad_stats_ms = (time.perf_counter() - t_grad) * 1000.0
-
-        if stats_tensor is not None:
-            dev = params_with_grad[0][0].device
-            avg_stats = stats_tensor.mean(dim=0)
-
-            if dist.is_available() and dist.is_initialized():
-                self._sync_device(dev)
-                t_ar = time.perf_counter()
-                dist.all_reduce(avg_stats, op=dist.ReduceOp.SUM)
-                avg_stats /= dist.get_world_size()
-                self._sync_device(dev)
-                allreduce_ms = (time.perf_counter() - t_ar) * 1000.0
-
-            self._sync_device(dev)
-            t_score = time.perf_counter()
-            if self.n_ema is None:
-                self.n_ema = avg_stats[0]
-                self.r_ema = avg_stats[1]
-                self.v_global_ema = avg_stats[2]
-            else:
-                alpha = self.param_groups[0]["alpha"]
-                self.n_ema = alpha * avg_stats[0] + (1 - alpha) * self.n_ema
-                self.r_ema = alpha * avg_stats[1] + (1 - alpha) * self.r_ema
-                self.v_global_ema = alpha * avg_stats[2] + (1 - alpha) * self.v_global_ema
-
-            tau = self.param_groups[0]["tau"]
-            states = [self.state[p] for p, _g in params_with_grad]
-            scores = self._scores(stats_tensor, [st["step"] for st in states], tau)
-            host_scores = scores.cpu().tolist()          # the step's one device -> host read
-            for (_p, g), st, sc, hs in zip(params_with_grad, states, scores.unbind(0), host_scores):
-                st["last_score"] = sc
-                if g.get("bits") is None:
-                    st["current_bit"] = self._score_to_bits(hs)
-            self._sync_device(dev)
-            score_bits_ms = (time.perf_counter() - t_score) * 1000.0
-
+        if decide and work and any(g.get("bits") is None for _p, g in work):
+            self._decide_bits(work)
         lt = self.last_step_timings
-        lt["mdq_grad_stats_ms"] = grad_stats_ms
-        lt["mdq_allreduce_ms"] = allreduce_ms
-        lt["mdq_score_bits_ms"] = score_bits_ms
-        lt["mdq_stats_ms"] = grad_stats_ms
-        lt["mdq_bit_decision_ms"] = allreduce_ms + score_bits_ms
-        lt["mdq_extra_stats_ms"] = grad_stats_ms + allreduce_ms + score_bits_ms
+        lt["mdq_stats_ms"] = lt["mdq_grad_stats_ms"]
+        lt["mdq_bit_decision_ms"] = lt["mdq_allreduce_ms"] + lt["mdq_score_bits_ms"]
+        lt["mdq_extra_stats_ms"] = lt["mdq_grad_stats_ms"] + lt["mdq_bit_decision_ms"]
 
-        # Phase profiling needs the cycle buffer read back (a device sync), so it
-        # is on only with sync_timing, as the reference always has it.
-        profile_device = None
-        if params_with_grad and self.sync_timing:
-            profile_device = params_with_grad[0][0].device
-            if profile_device.type == "cuda":
-                self._reset_kernel_profile(profile_device)
-
-        if params_with_grad:
-            self._batched_update(params_with_grad)
-
-        self._finalize_step_timings(
-            profile_device if profile_device is not None and profile_device.type == "cuda" else None
-        )
+        prof_dev = self._profile_device(work[0][0].device) if work else None
+        if work:
+            self._batched_update(work)
+        self._finalize_step_timings(prof_dev)
         return loss
 
-    def _batched_update(self, params_with_grad):
-        """All tensors: prepare (align storage), one launch per storage class,
-        re-pack; timing keys as the per-tensor loop of :501-502 fills them."""
-        dev = params_with_grad[0][0].device
-        t0 = time.perf_counter()
-        self._pending_align = [] if self._device_transitions else None
-        try:
-            repack = [self._prepare_update(p, g) for p, g in params_with_grad]
-        finally:
-            self._flush_align()
-        unpack_ms = (time.perf_counter() - t0) * 1000.0
-        if self.sync_timing:
-            self._sync_device(dev)
-        tk0 = time.perf_counter()
-        restores = self.__dict__.pop("_restores", None) or {}
-        if restores:
-            steady = [(p, g) for p, g in params_with_grad if id(p) not in restores]
-            runs = self._run_kernels(steady) if steady else []
-            self._run_restores(list(restores.values()))
-        else:
-            runs = self._run_kernels(params_with_grad)
-        if self.sync_timing:
-            self._sync_device(dev)
-        kernel_ms = (time.perf_counter() - tk0) * 1000.0
-        t1 = time.perf_counter()
-        self._pending_pack = [] if self._device_transitions else None
-        try:
-            for (p, _g), rp in zip(params_with_grad, repack):
-                if rp and id(p) not in restores:
-                    self._finish_update(p)
-        finally:
-            self._flush_pack()
-        pack_ms = (time.perf_counter() - t1) * 1000.0
-        lt = self.last_step_timings
-        lt["quant_dequant_unpack_ms"] += unpack_ms
-        lt["quant_dequant_kernel_ms"] += kernel_ms
-        lt["quant_dequant_pack_ms"] += pack_ms
-        # No storage was replaced: the plans just launched describe the state as
-        # it stands, so the next step can reuse them (``_steady_step``).
-        self._steady = self._make_steady(params_with_grad, runs) if runs and not any(repack) else None
+    # ------------------------------------------------------------------
+    # metrics / checkpoint (stquant_opt_simple.py:321-378)
+    # ------------------------------------------------------------------
+    def _widths(self):
+        """``(bits, numel)`` of every param that has a width."""
+        for group in self.param_groups:
+            for p in group["params"]:
+                st = self.state.get(p)
+                if st and "current_bit" in st:
+                    yield int(st["current_bit"]), p.numel()
+
+    @staticmethod
+    def _percent(counts: Counter) -> dict:
+        total = sum(counts.values())
+        out = {b: 0.0 for b in _REPORTED_WIDTHS}
+        if total:
+            out.update({b: (c / total) * 100.0 for b, c in ({b: 0 for b in _REPORTED_WIDTHS} | counts).items()})
+        return out
+
+    def get_bit_distribution(self):
+        """Percent of tensors at each width."""
+        return self._percent(Counter(b for b, _n in self._widths()))
+
+    def get_bit_distribution_param_weighted(self):
+        """Percent of parameters at each width."""
+        counts = Counter()
+        for b, n in self._widths():
+            counts[b] += n
+        return self._percent(counts)
+
+    def get_avg_bit_param_weighted(self):
+        share = self.get_bit_distribution_param_weighted()
+        return float(sum(b * (pc / 100.0) for b, pc in share.items()))
+
+    def get_all_raw_scores(self):
+        scores = [st["last_score"] for g in self.param_groups for p in g["params"]
+                  for st in (self.state.get(p),) if st and "last_score" in st]
+        if not scores:
+            return []
+        # one device read for all of them
+        return torch.stack([s.reshape(()).to(scores[0].device, torch.float64) for s in scores]).cpu().tolist()
+
+    def _global_stats(self) -> dict:
+        return {"n_ema": self.n_ema, "r_ema": self.r_ema, "v_global_ema": self.v_global_ema,
+                "total_steps": self.total_steps}
+
+    def state_dict(self):
+        return {**super().state_dict(), "mdq_global_stats": self._global_stats()}
+
+    def load_state_dict(self, state_dict):
+        """The reference's loader (stquant_opt_simple.py:371-378) with two repairs:
+        - torch's ``Optimizer.load_state_dict`` casts every floating-point param's state tensors to
+          the param dtype, which would turn the integer codes into float32 and lose the low bits of
+          32-bit codes.  The code tensors are therefore held back from torch's loader and put back
+          unchanged, on the param's device.
+        - torch moves per-param state to the param's device but not the global EMA statistics;
+          they are moved to the device of the first param (where the bit decision computes them),
+          so a checkpoint written on one device resumes on another."""
+        self._steady = None
+        self.__dict__.pop("_plan_cache", None)
+        sd = dict(state_dict)
+        stats = sd.pop("mdq_global_stats", None)
+        held = {}
+        sd["state"] = {}
+        for pid, st in state_dict.get("state", {}).items():
+            st = dict(st)
+            held[pid] = {k: st.pop(k) for k in _CODE_KEYS if k in st and torch.is_tensor(st[k])}
+            sd["state"][pid] = st
+        if stats is not None:
+            self.n_ema, self.r_ema = stats["n_ema"], stats["r_ema"]
+            self.v_global_ema, self.total_steps = stats["v_global_ema"], stats["total_steps"]
+        super().load_state_dict(sd)
+        params = [p for g in self.param_groups for p in g["params"]]
+        saved_ids = [pid for g in sd["param_groups"] for pid in g["params"]]
+        for pid, p in zip(saved_ids, params):
+            for k, t in held.get(pid, {}).items():
+                self.state[p][k] = t.to(p.device)
+        if params:
+            dev = params[0].device
+            for k in ("n_ema", "r_ema", "v_global_ema"):
+                v = getattr(self, k)
+                if torch.is_tensor(v) and v.device != dev:
+                    setattr(self, k, v.to(dev))
 
     # ------------------------------------------------------------------
     # steady state: same tensors, same storage, same bit widths as last step
@@ -884,7 +643,8 @@ class MDQAdamWSimple(Optimizer):
         same ``state`` dict, the same per-group bits / block size / rounding /
         seed, and no bit decision this step (scored groups re-decide bits on
         update steps).  Storage is only replaced by steps that re-pack, by
-        ``load_state_dict`` and by ``add_param_group``, which all drop the cache.
+        ``load_state_dict`` and by ``add_param_group``, which all drop the cache;
+        a param whose ``data`` moved is caught by ``_steady_step``.
         """
         sc = self.__dict__.get("_steady")
         if sc is None or sc["state_obj"] is not self.state:
@@ -899,13 +659,14 @@ class MDQAdamWSimple(Optimizer):
         return sc
 
     def _steady_step(self, sc) -> bool:
-        """One step over the cached plans: ``step += 1`` per tensor, fresh grad
-        pointers, steps and per-group hyper-parameters; False (nothing launched,
-        nothing changed) if a grad no longer matches its plan."""
+        """One step over the cached plans: ``step += 1`` per tensor, fresh param and grad
+        pointers, steps and per-group hyper-parameters; False (nothing launched, nothing
+        changed) if a param or grad no longer matches its plan."""
         params, states = sc["params"], sc["states"]
         t0 = time.perf_counter()
         for plan, idx, _gidx in sc["runs"]:
-            if not plan.try_set_grads([params[i].grad for i in idx]):
+            sel = [params[i] for i in idx]
+            if not plan.try_set_params(sel) or not plan.try_set_grads([p.grad for p in sel]):
                 return False
         steps = []
         for st in states:
@@ -920,29 +681,26 @@ class MDQAdamWSimple(Optimizer):
         wd = np.array([g["weight_decay"] for g in groups], np.float32)
         unpack_ms = (time.perf_counter() - t0) * 1000.0
         dev = params[0].device
-        prof = None
-        if self.sync_timing and self._kernel_profile_buf is not None and self._kernel_profile_device == dev:
-            prof = self._kernel_profile_buf
-        if self.sync_timing:
-            self._sync_device(dev)
-        tk0 = time.perf_counter()
-        for plan, idx, gidx in sc["runs"]:
-            a = plan.arr
-            a["step"] = steps[idx]
-            a["lr"] = lr[gidx]
-            a["beta1"] = b1[gidx]
-            a["beta2"] = b2[gidx]
-            a["eps"] = eps[gidx]
-            a["weight_decay"] = wd[gidx]
-            plan.run(prof)
-        if self.sync_timing:
-            self._sync_device(dev)
-        kernel_ms = (time.perf_counter() - tk0) * 1000.0
+        prof = self._profile.active(dev) if self.sync_timing else None
+        with _Stopwatch(dev, self.sync_timing) as sw:
+            for plan, idx, gidx in sc["runs"]:
+                a = plan.arr
+                a["step"] = steps[idx]
+                a["lr"] = lr[gidx]
+                a["beta1"] = b1[gidx]
+                a["beta2"] = b2[gidx]
+                a["eps"] = eps[gidx]
+                a["weight_decay"] = wd[gidx]
+                plan.run(prof)
         lt = self.last_step_timings
         lt["quant_dequant_unpack_ms"] += unpack_ms
-        lt["quant_dequant_kernel_ms"] += kernel_ms
+        lt["quant_dequant_kernel_ms"] += sw.ms
         self._count_steady_params(len(states))
         return True
 
     def _count_steady_params(self, n: int) -> None:
         """Per-tensor bookkeeping a steady step skips (FusedIO counts fast-path tensors)."""
+
+
+_STATE_TENSORS = ("exp_avg", "exp_avg_sq", "scale_m", "scale_v", "v_min")
+_CODE_KEYS = ("exp_avg", "exp_avg_sq")

@@ -1,14 +1,15 @@
-"""Code-storage conversion on the GPU (stq_multi_tensor_convert_codes) against the reference's own
-torch restatement of the storage changes (MDQAdamWSimple._align_momentum_storage /
-_pack_momentum_storage, stquant_opt_simple.py:140-219) run on CPU copies: every source storage x
-every target bit width, codes spanning each source type's full range (so every clamp is hit),
-sizes around the 4096-element tile, several tensors per launch.  Bit-exact."""
+"""Code-storage conversion on the GPU (stq_multi_tensor_convert_codes) against the element-wise
+model of the reference's storage rules on a bit-width change (tests/storage_model.py,
+stquant_opt_simple.py:140-219): every source storage x every target bit width, codes spanning
+each source type's full range (so every clamp is hit), sizes around the 4096-element tile,
+several tensors per launch.  Bit-exact."""
 import numpy as np
 import pytest
 import torch
 
 import mdq_hip
-from stquant_opt_simple import MDQAdamWSimple
+from mdq_hip import storage
+from storage_model import after_kernel, before_kernel, model_arrays
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -37,6 +38,14 @@ def as_i64(t):
     return t.to(torch.int64)
 
 
+def _model(fn, src, cm, cv, bits):
+    """The storage model applied to CPU codes of layout ``src`` (a storage constant or a SRC key)."""
+    src = _STORE.get(src, src)
+    m = as_i64(cm).numpy()
+    v = np.zeros_like(m) if src == storage.STORE_P4 else as_i64(cv).numpy()
+    return model_arrays(fn, src, m, v, bits)
+
+
 @pytest.mark.parametrize("src", list(SRC))
 @pytest.mark.parametrize("bits", [4, 8, 16, 32])
 def test_align_matches_reference(src, bits):
@@ -44,29 +53,25 @@ def test_align_matches_reference(src, bits):
     states, items, want = [], [], []
     for k, n in enumerate(SIZES):
         cm, cv = rand_codes(src, n, 100 * bits + k)
-        ref = {"exp_avg": cm.clone(), "exp_avg_sq": cv.clone()}
-        MDQAdamWSimple._align_momentum_storage(ref, bits)
-        want.append(ref)
+        want.append(_model(before_kernel, src, cm, cv, bits))
         gm, gv = cm.to(DEV), cv.to(DEV)
-        dst = MDQAdamWSimple._aligned_storage(bits)
+        dst = storage.kernel_layout(bits)
         nm, nv = mdq_hip.empty_codes(gm, dst)
         items.append((gm, gv, nm, nv))
         states.append((nm, nv))
     mdq_hip.convert_codes(items)
     torch.cuda.synchronize()
-    for (nm, nv), ref, n in zip(states, want, SIZES):
-        assert nm.dtype == ref["exp_avg"].dtype and nv.dtype == ref["exp_avg_sq"].dtype, (n, nm.dtype, nv.dtype)
-        assert torch.equal(as_i64(nm.cpu()), as_i64(ref["exp_avg"])), f"m codes, n={n}"
-        assert torch.equal(as_i64(nv.cpu()), as_i64(ref["exp_avg_sq"])), f"v codes, n={n}"
+    for (nm, nv), (lay, m, v), n in zip(states, want, SIZES):
+        assert storage.layout_of(nm, nv) == lay, (n, nm.dtype, nv.dtype)
+        assert np.array_equal(as_i64(nm.cpu()).numpy(), m), f"m codes, n={n}"
+        assert np.array_equal(as_i64(nv.cpu()).numpy(), v), f"v codes, n={n}"
 
 
 def test_pack_to_nibbles_matches_reference():
     items, want, outs = [], [], []
     for k, n in enumerate(SIZES):
         cm, cv = rand_codes("s8", n, 7 + k)
-        ref = {"exp_avg": cm.clone(), "exp_avg_sq": cv.clone()}
-        MDQAdamWSimple._pack_momentum_storage(ref, 4)
-        want.append(ref["exp_avg"])
+        want.append(_model(after_kernel, storage.STORE_S8, cm, cv, 4)[1])
         gm, gv = cm.to(DEV), cv.to(DEV)
         nm, nv = mdq_hip.empty_codes(gm, mdq_hip.STORE_P4)
         items.append((gm, gv, nm, nv))
@@ -75,11 +80,10 @@ def test_pack_to_nibbles_matches_reference():
     torch.cuda.synchronize()
     for (nm, nv), w, n in zip(outs, want, SIZES):
         assert nm.dtype == torch.uint8 and nv.numel() == 0
-        assert torch.equal(nm.cpu(), w), f"n={n}"
+        assert np.array_equal(nm.cpu().numpy().astype(np.int64), w), f"n={n}"
 
 
 def test_empty_tensors_are_a_no_op():
-    # (the optimizer keeps the reference's torch path for empty tensors, whose dtype rules differ)
     e8, e16 = torch.empty(0, dtype=torch.int8, device=DEV), torch.empty(0, dtype=torch.int16, device=DEV)
     out = mdq_hip.empty_codes(e16, mdq_hip.STORE_S8)
     mdq_hip.convert_codes([(e16, torch.empty(0, dtype=torch.uint16, device=DEV), *out),

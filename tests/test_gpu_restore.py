@@ -17,6 +17,7 @@ import pytest
 import torch
 
 import mdq_hip
+from mdq_hip import storage
 from stquant_opt_fused_io import MDQAdamWSimpleFusedIO
 from stquant_opt_simple import MDQAdamWSimple
 from test_gpu_optimizer import build, grads
@@ -83,7 +84,7 @@ class Tensors:
 def separate_passes(t, dst, B, rounding, seed, step):
     """convert to the aligned storage -> step kernel at the new width -> pack nibbles."""
     bits = BITS[dst]
-    aligned = MDQAdamWSimple._aligned_storage(bits)
+    aligned = storage.kernel_layout(bits)
     moves = []
     for it in t.items:
         if mdq_hip.storage_of(it[2], it[3]) != aligned:
