@@ -9,6 +9,11 @@
  * Return value: STQ_OK, or an STQ_ERR_* code with a message available from
  * stq_last_error() (thread-local).  Argument errors are reported before any
  * device work is queued.
+ *
+ * The multi-tensor entry points upload a descriptor table per call from
+ * staging buffers that later calls reuse, so they refuse (STQ_ERR_INVALID,
+ * nothing queued) a stream that is capturing a HIP graph: a replay of such a
+ * capture would launch with another call's descriptors.
  */
 #ifndef STQUANT_HIP_H
 #define STQUANT_HIP_H

@@ -250,6 +250,23 @@ int take_slot(DevCtx *ctx, size_t need, Slot **out)
     return STQ_OK;
 }
 
+// Descriptor tables are uploaded from a ring of staging slots that later
+// calls refill, so a call captured into a HIP graph would, on replay, launch
+// with whatever another call left in its slot.  Every entry point that uploads
+// refuses a capturing stream before any slot, event or device work.
+int refuse_capture(hipStream_t stream)
+{
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    const hipError_t e = hipStreamIsCapturing(stream, &cs);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
+    if (cs != hipStreamCaptureStatusNone)
+        return fail(STQ_ERR_INVALID,
+                    "the stream is capturing a HIP graph: this library uploads each call's descriptor table "
+                    "from staging buffers that later calls reuse, so a replay would step other tensors; "
+                    "call it outside graph capture");
+    return STQ_OK;
+}
+
 // Copies the first `bytes` of the slot's staging buffer to its device buffer
 // so that work queued next on `stream` sees them.  The copy goes on the
 // device's copy stream and `stream` waits for it: a copy queued on `stream`
@@ -261,17 +278,13 @@ int take_slot(DevCtx *ctx, size_t need, Slot **out)
 // microseconds) gets the copy on `stream` itself: there the cross-stream wait
 // costs more than the overlap saves (flat 4M-element step 26.5 -> 17.7 us per
 // call; GPT-2 small, 124M elements, 277 us per call with the copy stream, 286
-// without; LLaMA-7B level).  So does a stream under graph capture.  Called
-// with ctx->mu held.
+// without; LLaMA-7B level).  Called with ctx->mu held.
 constexpr int64_t SMALL_LAUNCH_ELEMS = int64_t(1) << 24;
 
 int upload(DevCtx *ctx, Slot &s, size_t bytes, int64_t elems, hipStream_t stream)
 {
     hipError_t e;
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    e = hipStreamIsCapturing(stream, &cs);
-    if (e != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
-    const bool on_stream = cs != hipStreamCaptureStatusNone || elems < SMALL_LAUNCH_ELEMS;
+    const bool on_stream = elems < SMALL_LAUNCH_ELEMS;
     if (!on_stream && !ctx->copy_stream) {
         e = hipStreamCreateWithFlags(&ctx->copy_stream, hipStreamNonBlocking);
         if (e != hipSuccess) {
@@ -307,8 +320,10 @@ int release_slot(Slot *s, hipStream_t stream)
 int upload_and_launch(const std::vector<MdqDesc> &descs, int src_storage, int storage, int grad_dt, int log2b,
                       bool sr, int64_t total_tiles, unsigned long long *prof, uint64_t seed, hipStream_t stream)
 {
+    int rc = refuse_capture(stream);
+    if (rc != STQ_OK) return rc;
     DevCtx *ctx = nullptr;
-    int rc = get_ctx(&ctx);
+    rc = get_ctx(&ctx);
     if (rc != STQ_OK) return rc;
     std::lock_guard<std::mutex> lk(ctx->mu);
     const size_t n = descs.size();
@@ -371,14 +386,16 @@ int run_grad_stats(const void *const *grads, const int64_t *numels, int n, int g
     }
     if (tiles > 0x7fffffffLL)
         return fail(STQ_ERR_INVALID, "too many tiles in one call (%lld); split the tensor list", (long long)tiles);
+    int rc = refuse_capture(stream);
+    if (rc != STQ_OK) return rc;
     DevCtx *ctx = nullptr;
-    int rc = get_ctx(&ctx);
+    rc = get_ctx(&ctx);
     if (rc != STQ_OK) return rc;
     std::lock_guard<std::mutex> lk(ctx->mu);
     const size_t up = (size_t)n * (sizeof(mdq::StatDesc) + sizeof(long long));
     const size_t part_off = (up + 255) / 256 * 256;
     Slot *s = nullptr;
-    rc = take_slot(ctx, part_off + (size_t)tiles * 3 * sizeof(double), &s);
+    rc = take_slot(ctx, part_off + (size_t)tiles * mdq::STAT_PARTIALS * sizeof(double), &s);
     if (rc != STQ_OK) return rc;
     std::memcpy(s->host, d.data(), (size_t)n * sizeof(mdq::StatDesc));
     long long *tb = reinterpret_cast<long long *>(s->host + (size_t)n * sizeof(mdq::StatDesc));
@@ -579,8 +596,10 @@ int run_convert(const stq_code_convert *items, int n, hipStream_t stream)
     if (d.empty()) return STQ_OK;
     if (tiles > 0x7fffffffLL)
         return fail(STQ_ERR_INVALID, "too many tiles in one call (%lld); split the tensor list", (long long)tiles);
+    int rc = refuse_capture(stream);
+    if (rc != STQ_OK) return rc;
     DevCtx *ctx = nullptr;
-    int rc = get_ctx(&ctx);
+    rc = get_ctx(&ctx);
     if (rc != STQ_OK) return rc;
     std::lock_guard<std::mutex> lk(ctx->mu);
     const size_t m = d.size();
