@@ -225,16 +225,33 @@ def init_state(n: int, block_size: int, storage: int):
 def grad_stats(g: np.ndarray) -> np.ndarray:
     """``stquant_opt_simple.py:93-98`` restated for one gradient: float32
     ``[sqrt(mean(g^2)), std(g) / (mean(|g|) + 1e-12), mean(g^2)]`` with the
-    unbiased std, sums in float64 (two-pass variance), then the reference's
-    final fp32 operations (sqrt of the fp32 mean, fp32 divide and add).
-    numel 0 gives NaN means; numel 1 a NaN std, as torch does."""
-    x = np.asarray(g, dtype=np.float64).ravel()
+    unbiased std.  Each square is rounded to fp32 (the reference's ``grad * grad``);
+    the sums are float64, the variance two-pass; then the reference's final fp32
+    operations (sqrt of the fp32 mean, fp32 divide and add).  The reference sums in
+    fp32 on the GPU (torch's mean, and its Welford std), so a sum of squares, of
+    absolute values or of squared deviations whose exact value exceeds FLT_MAX gives
+    inf.  numel 0 gives NaN means; numel 0 or 1 a NaN std, as torch does."""
+    x32 = np.asarray(g, dtype=np.float32).ravel()
+    x = x32.astype(np.float64)
     n = x.size
     nan = np.float32(np.nan)
+    big = float(np.finfo(np.float32).max)
+
+    def f32_mean(total, count):
+        # the fp32 accumulator overflows once the exact sum exceeds FLT_MAX
+        return np.float32(np.inf) if total > big else np.float32(total / count)
+
     with np.errstate(all="ignore"):
-        mean_sq = np.float32(np.sum(x * x) / n) if n else nan
-        mean_abs = np.float32(np.sum(np.abs(x)) / n) if n else nan
-        sd = np.float32(np.sqrt(np.var(x, ddof=1))) if n > 1 else nan
+        if n:
+            mean_sq = f32_mean(float(np.sum((x32 * x32).astype(np.float64))), n)
+            mean_abs = f32_mean(float(np.sum(np.abs(x))), n)
+        else:
+            mean_sq = mean_abs = nan
+        if n > 1:
+            m2 = float(np.sum((x - np.sum(x) / n) ** 2))
+            sd = np.float32(np.inf) if m2 > big else np.float32(np.sqrt(m2 / (n - 1)))
+        else:
+            sd = nan
         n_l = np.sqrt(mean_sq, dtype=np.float32)
         r_l = np.float32(sd / np.float32(mean_abs + np.float32(1e-12)))
     return np.array([n_l, r_l, mean_sq], dtype=np.float32)

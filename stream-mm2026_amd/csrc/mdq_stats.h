@@ -8,6 +8,7 @@ namespace mdq {
 
 // Elements per workgroup tile of the partial-sum kernel (512 threads x 64).
 constexpr int STAT_TILE = 32768;
+constexpr int STAT_PARTIALS = 4;   // doubles per tile
 
 // One tensor of a statistics launch: tiles [tile_begin, tile_end) of the
 // launch cover its numel elements (none when numel == 0).
@@ -20,7 +21,8 @@ struct alignas(16) StatDesc {
 
 static_assert(sizeof(StatDesc) == 32, "StatDesc layout");
 
-// partials: 3 doubles per tile; out: 3 floats per tensor (n_l, r_l, v_l).
+// partials: 4 doubles per tile (sum g, sum of squared deviations from the tile
+// mean, sum g^2, sum |g|); out: 3 floats per tensor (n_l, r_l, v_l).
 hipError_t launch_grad_stats(const StatDesc *d, const long long *tile_begin, int n, long long tiles,
                              int grad_dt, double *partials, float *out, hipStream_t s);
 

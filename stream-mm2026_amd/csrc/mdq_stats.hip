@@ -3,12 +3,19 @@
 //
 // The reference computes, per tensor and before the step (stquant_opt_simple.py:93-98),
 //   n_l = sqrt(mean(g^2)),  r_l = std(g) / (mean(|g|) + 1e-12),  v_l = mean(g^2)
-// with std unbiased, as separate torch reductions per tensor.  Here:
-//   1. stats_partial_kernel: one 512-thread workgroup per 32768-element tile of one tensor
-//      accumulates sum g, sum g^2, sum |g| in fp64 (each fp32 square is exact
-//      in fp64) and writes the three partial sums of its tile;
-//   2. stats_finish_kernel: one workgroup per tensor adds its tiles' partials
-//      in a fixed order and rounds to the reference's fp32 outputs.
+// with std unbiased, as separate fp32 torch reductions per tensor.  Here:
+//   1. stats_partial_kernel: one 512-thread workgroup per 32768-element tile of
+//      one tensor.  It holds the tile in registers and writes four fp64 partials:
+//      - sum g;
+//      - sum (g - tile mean)^2, from a second pass over the registers;
+//      - sum g^2, each square rounded to fp32 as the reference's grad * grad is;
+//      - sum |g|.
+//   2. stats_finish_kernel: one workgroup per tensor combines its tiles in a fixed
+//      order.  The squared deviations combine by Chan's pairwise formula,
+//      M2 = sum M2_i + sum n_i (mean_i - mean)^2, which stays exact to fp64
+//      rounding however large |mean| is against the spread.  The results are
+//      rounded to the reference's fp32 outputs.  A sum whose exact value exceeds
+//      FLT_MAX gives inf, as the reference's fp32 accumulators overflow.
 // Both orders are fixed by the tensor list, so results are deterministic.
 #include <hip/hip_runtime.h>
 
@@ -58,41 +65,36 @@ __device__ __forceinline__ void load_vec(const void *g, int64_t e, float (&x)[ve
     }
 }
 
+// fp64 sums of one element: g, g^2 (the fp32 square), |g|
 __device__ __forceinline__ void acc(double &s1, double &s2, double &sa, float x)
 {
-    const double d = (double)x;
-    s1 += d;
-    s2 = fma(d, d, s2);
-    sa += fabs(d);
+    s1 += (double)x;
+    s2 += (double)(x * x);
+    sa += fabs((double)x);
 }
 
-// Sum of three doubles over the workgroup; the result is valid in thread 0.
-__device__ __forceinline__ void block_sum3(double &s1, double &s2, double &sa, double (*lds)[3])
+// Sum of K doubles over the workgroup; the totals are returned in every thread
+// (through LDS), summed in a fixed order.
+template <int K>
+__device__ __forceinline__ void block_sum(double (&v)[K], double (*lds)[K])
 {
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        s1 += __shfl_xor(s1, off, 64);
-        s2 += __shfl_xor(s2, off, 64);
-        sa += __shfl_xor(sa, off, 64);
-    }
-    const int w = threadIdx.x / 64;
-    if ((threadIdx.x & 63) == 0) {
-        lds[w][0] = s1;
-        lds[w][1] = s2;
-        lds[w][2] = sa;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        s1 = lds[0][0];
-        s2 = lds[0][1];
-        sa = lds[0][2];
+    for (int off = 32; off >= 1; off >>= 1)
 #pragma unroll
-        for (int k = 1; k < ST_WAVES; ++k) {
-            s1 += lds[k][0];
-            s2 += lds[k][1];
-            sa += lds[k][2];
-        }
+        for (int k = 0; k < K; ++k) v[k] += __shfl_xor(v[k], off, 64);
+    const int w = threadIdx.x / 64;
+    if ((threadIdx.x & 63) == 0)
+#pragma unroll
+        for (int k = 0; k < K; ++k) lds[w][k] = v[k];
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        double t = lds[0][k];
+#pragma unroll
+        for (int q = 1; q < ST_WAVES; ++q) t += lds[q][k];
+        v[k] = t;
     }
+    __syncthreads();   // lds is free for the next block_sum
 }
 
 template <int GT>
@@ -100,7 +102,8 @@ __global__ __launch_bounds__(ST_THREADS) void stats_partial_kernel(const StatDes
                                                                    const long long *__restrict__ tb,
                                                                    double *__restrict__ partials)
 {
-    __shared__ double lds[ST_WAVES][3];
+    __shared__ double lds3[ST_WAVES][3];
+    __shared__ double lds1[ST_WAVES][1];
     // Workgroup b runs on XCD x = b % 8 as its j-th (j = b / 8); the tiles go to
     // the XCDs in round-robin chunks of 16 (2^19 elements), the workgroups of the
     // last, partial round of 8 chunks take tile b (a bijection on [0, grid)).
@@ -119,55 +122,93 @@ __global__ __launch_bounds__(ST_THREADS) void stats_partial_kernel(const StatDes
     }
     const StatDesc t = d[lo];
     const int64_t base = (tile - t.tile_begin) * STAT_TILE;
-    double s1 = 0.0, s2 = 0.0, sa = 0.0;
-    const bool vec = base + STAT_TILE <= t.numel && (reinterpret_cast<uintptr_t>(t.g) % 16) == 0;
+    const int64_t cnt = t.numel - base < STAT_TILE ? t.numel - base : STAT_TILE;   // elements of this tile
+    double s[3] = {0.0, 0.0, 0.0};      // sum g, sum g^2, sum |g|
+    double m2[1] = {0.0};               // sum (g - tile mean)^2
+    const bool vec = cnt == STAT_TILE && (reinterpret_cast<uintptr_t>(t.g) % 16) == 0;
     if (vec) {
-        // all loads of the thread first (STAT_TILE / ST_THREADS elements), then the sums
+        // the whole tile in registers (STAT_TILE / ST_THREADS elements per thread):
+        // one pass for the sums, a second over the registers for the deviations
         constexpr int V = vec_elems<GT>();
         constexpr int NL = STAT_TILE / (V * ST_THREADS);
-        float x[NL][V];
+        float xv[NL][V];
 #pragma unroll
-        for (int k = 0; k < NL; ++k) load_vec<GT>(t.g, base + V * ((int64_t)k * ST_THREADS + threadIdx.x), x[k]);
+        for (int k = 0; k < NL; ++k) load_vec<GT>(t.g, base + V * ((int64_t)k * ST_THREADS + threadIdx.x), xv[k]);
 #pragma unroll
         for (int k = 0; k < NL; ++k)
 #pragma unroll
-            for (int j = 0; j < V; ++j) acc(s1, s2, sa, x[k][j]);
+            for (int e = 0; e < V; ++e) acc(s[0], s[1], s[2], xv[k][e]);
+        block_sum<3>(s, lds3);
+        const double mean = s[0] / (double)STAT_TILE;
+#pragma unroll
+        for (int k = 0; k < NL; ++k)
+#pragma unroll
+            for (int e = 0; e < V; ++e) {
+                const double dv = (double)xv[k][e] - mean;
+                m2[0] = fma(dv, dv, m2[0]);
+            }
     } else {
         for (int k = 0; k < STAT_TILE / ST_THREADS; ++k) {
-            const int64_t e = base + (int64_t)k * ST_THREADS + threadIdx.x;
-            if (e < t.numel) acc(s1, s2, sa, load_one<GT>(t.g, e));
+            const int64_t e = (int64_t)k * ST_THREADS + threadIdx.x;
+            if (e < cnt) acc(s[0], s[1], s[2], load_one<GT>(t.g, base + e));
+        }
+        block_sum<3>(s, lds3);
+        const double mean = s[0] / (double)cnt;
+        for (int k = 0; k < STAT_TILE / ST_THREADS; ++k) {
+            const int64_t e = (int64_t)k * ST_THREADS + threadIdx.x;
+            if (e < cnt) {
+                const double dv = (double)load_one<GT>(t.g, base + e) - mean;
+                m2[0] = fma(dv, dv, m2[0]);
+            }
         }
     }
-    block_sum3(s1, s2, sa, lds);
+    block_sum<1>(m2, lds1);
     if (threadIdx.x == 0) {
-        partials[3 * tile + 0] = s1;
-        partials[3 * tile + 1] = s2;
-        partials[3 * tile + 2] = sa;
+        partials[4 * tile + 0] = s[0];
+        partials[4 * tile + 1] = m2[0];
+        partials[4 * tile + 2] = s[1];
+        partials[4 * tile + 3] = s[2];
     }
 }
+
+// fp32 value of a sum of non-negative terms as an fp32 accumulator holds it:
+// inf once the exact sum exceeds FLT_MAX.
+__device__ __forceinline__ float f32_sum(double x) { return x > (double)__FLT_MAX__ ? __builtin_inff() : (float)x; }
 
 __global__ __launch_bounds__(ST_THREADS) void stats_finish_kernel(const StatDesc *__restrict__ d,
                                                                   const double *__restrict__ partials,
                                                                   float *__restrict__ out)
 {
-    __shared__ double lds[ST_WAVES][3];
+    __shared__ double lds3[ST_WAVES][3];
+    __shared__ double lds1[ST_WAVES][1];
     const StatDesc t = d[blockIdx.x];
-    double s1 = 0.0, s2 = 0.0, sa = 0.0;
+    double s[3] = {0.0, 0.0, 0.0};      // sum g, sum g^2, sum |g|
     for (long long k = t.tile_begin + threadIdx.x; k < t.tile_end; k += ST_THREADS) {
-        s1 += partials[3 * k + 0];
-        s2 += partials[3 * k + 1];
-        sa += partials[3 * k + 2];
+        s[0] += partials[4 * k + 0];
+        s[1] += partials[4 * k + 2];
+        s[2] += partials[4 * k + 3];
     }
-    block_sum3(s1, s2, sa, lds);
+    block_sum<3>(s, lds3);
+    const double N = (double)t.numel;
+    const double mean = s[0] / N;
+    // Chan et al.'s combination of the tiles' (count, mean, M2)
+    double m2[1] = {0.0};
+    for (long long k = t.tile_begin + threadIdx.x; k < t.tile_end; k += ST_THREADS) {
+        const int64_t first = (k - t.tile_begin) * STAT_TILE;
+        const double ni = (double)(t.numel - first < STAT_TILE ? t.numel - first : STAT_TILE);
+        const double dm = partials[4 * k + 0] / ni - mean;
+        m2[0] += fma(ni * dm, dm, partials[4 * k + 1]);
+    }
+    block_sum<1>(m2, lds1);
     if (threadIdx.x == 0) {
-        // fp32 outputs in the reference's operation order: mean and std are fp32
-        // tensors, then sqrt / divide / add in fp32.  numel 0 gives NaN means and
-        // numel 1 a NaN std (unbiased), as torch does.
-        const double N = (double)t.numel;
-        const float mean_sq = (float)(s2 / N);
-        const float mean_abs = (float)(sa / N);
-        const double var = (s2 - s1 * (s1 / N)) / (N - 1.0);
-        const float sd = (float)sqrt(var > 0.0 ? var : (var == var ? 0.0 : var));
+        // The reference's fp32 results: mean(g * g) and mean(|g|) from fp32 sums, std from
+        // an fp32 M2 (torch's Welford accumulators on the GPU), then sqrt / divide / add in
+        // fp32.  numel 0 gives NaN means and numel 0 or 1 a NaN std (unbiased), as torch does.
+        const float sum_sq = f32_sum(s[1]), sum_abs = f32_sum(s[2]), m2f = f32_sum(m2[0]);
+        const float mean_sq = sum_sq == __builtin_inff() ? sum_sq : (float)(s[1] / N);
+        const float mean_abs = sum_abs == __builtin_inff() ? sum_abs : (float)(s[2] / N);
+        const float sd = t.numel < 2 ? __builtin_nanf("")
+                                     : (m2f == __builtin_inff() ? m2f : (float)sqrt(m2[0] / (N - 1.0)));
         out[3 * blockIdx.x + 0] = sqrtf(mean_sq);
         out[3 * blockIdx.x + 1] = sd / (mean_abs + 1e-12f);
         out[3 * blockIdx.x + 2] = mean_sq;

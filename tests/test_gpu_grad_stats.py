@@ -3,7 +3,11 @@
 - ``mdq_hip.grad_stats`` against the oracle (float64 sums, tests/test_oracle_grad_stats.py)
   within 1e-6 relative, over ragged sizes (tile edges at 16384 and 32768), fp32/bf16/fp16 and
   unaligned views; NaN where torch gives NaN (numel 0 and 1), NaN / inf where NaN / inf grads or
-  overflowing squares make them;
+  overflowing fp32 sums make them, as torch's fp32 reductions on the GPU do;
+- the variance exact for tensors whose mean dwarfs their spread (closed form);
+- over 320 tensors (zero-mean heavy-tailed, nonzero-mean, near-constant, outliers; 54 of them
+  scaled to sit 3e-4 .. 3e-2 from the 6.8 / 12 / 24 thresholds) the fused statistics give the
+  widths the reference's torch expression gives, and so does the optimizer over six steps;
 - deterministic (bit-identical on repeat), and within 1e-5 of the reference's fp32 torch
   reductions run on the same device;
 - ``MDQAdamWSimple._scores`` (one [n] vector) bit-identical to the reference's per-tensor
@@ -64,6 +68,7 @@ def test_nonfinite_grads_match_oracle(dtype):
     vs[10][50] = float("-inf")
     if dtype == torch.float32:
         vs[11][2] = 3e38
+        vs[12][:10] = 1e19                      # finite squares whose fp32 sum overflows
     got = mdq_hip.grad_stats(vs).cpu().numpy()
     for i, v in enumerate(vs):
         ref = orc.grad_stats(v.float().cpu().numpy())
@@ -133,3 +138,135 @@ def test_optimizer_fused_stats_same_decisions():
         assert lt["mdq_update_decision"] == (t % 2 == 0 or t < 5)
     bits = {oa.state[p]["current_bit"] for p in pa}
     print(f"bits chosen: {sorted(bits)}", flush=True)
+
+
+@pytest.mark.parametrize("case", ["nan", "inf", "square overflows", "sum of squares overflows"])
+def test_nonfinite_patterns_match_torch_on_the_gpu(case):
+    """The NaN / inf entries torch's fp32 reductions give on the GPU (the reference's platform)
+    for the same gradient, including r_l when an fp32 accumulator overflows."""
+    g = (torch.randn(100_000, generator=torch.Generator().manual_seed(4)) * 1e-3).to(DEV)
+    if case == "nan":
+        g[77] = float("nan")
+    elif case == "inf":
+        g[5] = float("inf")
+    elif case == "square overflows":
+        g[2] = 3e38
+    else:
+        g[:10] = 1e19
+    got = mdq_hip.grad_stats([g]).cpu().numpy()[0]
+    ref = MDQAdamWSimple._compute_grad_stats(g).cpu().numpy()
+    print(f"case {case}: kernel {got}, torch on the GPU {ref}", flush=True)
+    assert np.array_equal(np.isnan(got), np.isnan(ref)) and np.array_equal(np.isinf(got), np.isinf(ref)), (got, ref)
+
+
+@pytest.mark.parametrize("c_exp", [10, 20, 30])
+def test_variance_exact_for_large_means(c_exp):
+    """x = c + d (i mod 16), d the fp32 spacing at c, over 100,003 elements (four tiles, a
+    ragged one): unbiased var = d^2 (255 / 12) N / (N - 1) whatever c is."""
+    n = 100_003
+    c = float(2 ** c_exp)
+    d = float(np.spacing(np.float32(c)))
+    x = torch.from_numpy((c + d * (np.arange(n) % 16)).astype(np.float32)).to(DEV)
+    got = mdq_hip.grad_stats([x]).cpu().numpy()[0]
+    k = np.arange(n) % 16
+    mean = c + d * k.mean()
+    var = d * d * float(np.sum((k - k.mean()) ** 2)) / (n - 1)
+    sd = np.float32(np.sqrt(var))
+    want = np.float32(sd / np.float32(np.float32(mean) + np.float32(1e-12)))
+    assert abs(float(got[1]) - float(want)) <= 2e-7 * float(want), (got[1], want)
+    np.testing.assert_allclose(got[1], orc.grad_stats(x.cpu().numpy())[1], rtol=1e-6)
+
+
+SIZES_320 = [int(np.exp(u)) for u in np.random.default_rng(5).uniform(np.log(2), np.log(2 ** 15), 320)]
+
+
+def _many_grads(seed, sizes=SIZES_320):
+    """Gradients of four kinds (tensor i gets kind i mod 4): zero-mean Student-t(3), nonzero
+    mean (5x the spread), near-constant (spread 1e-5 of the mean), and Student-t with 0.1 %
+    outliers x1000; 320 sizes log-uniform in [2, 2^15]."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i, n in enumerate(sizes):
+        kind = i % 4
+        t = rng.standard_t(3, n) * 1e-3
+        if kind == 1:
+            t = t + 5e-3 * np.sign(rng.standard_normal())
+        elif kind == 2:
+            t = 2e-3 * (1 + 1e-5 * rng.standard_normal(n))
+        elif kind == 3:
+            t[rng.random(n) < 1e-3] *= 1000.0
+        out.append(torch.from_numpy(t.astype(np.float32)).to(DEV))
+    return out
+
+
+def _ref_stats(grads):
+    return torch.stack([MDQAdamWSimple._compute_grad_stats(g.float()) for g in grads])
+
+
+def test_widths_match_the_reference_near_thresholds():
+    print("case: bit decision over 320 tensors, 54 near a threshold", flush=True)
+    grads = _many_grads(11)
+    params = [torch.nn.Parameter(torch.zeros(1, device=DEV))]
+    opt = MDQAdamWSimple(params, layer_count=12, batch_size=8)
+    ema = _ref_stats(grads).float().nanmedian(dim=0).values
+    opt.n_ema, opt.r_ema, opt.v_global_ema = ema.unbind(0)
+    tau = opt.param_groups[0]["tau"]
+    steps = [1 + (7 * i) % 400 for i in range(len(grads))]
+
+    def ref_scores():
+        return opt._scores(_ref_stats(grads), steps, tau)
+
+    # scale 54 tensors so that the reference scores sit at threshold + delta: n_l scales with
+    # the grads, v_l with their square, r_l not at all, so a factor k moves the score by 3 log2 k
+    targets = [t + dl for t in (6.8, 12.0, 24.0) for dl in (-3e-2, -3e-3, -3e-4, 3e-4, 3e-3, 3e-2)]
+    picks = [i for i in range(len(grads)) if i % 4 != 2][:3 * len(targets):3]
+    for _ in range(3):
+        sc = ref_scores().cpu().numpy()
+        for i, tgt in zip(picks, targets):
+            grads[i] = grads[i] * float(2.0 ** ((tgt - sc[i]) / 3.0))
+    ref = ref_scores().cpu().numpy()
+    fused = opt._scores(mdq_hip.grad_stats(grads), steps, tau).cpu().numpy()
+    dist = min(abs(float(ref[i]) - t) for i in range(len(grads)) for t in (6.8, 12.0, 24.0))
+    print(f"max |score fused - score torch| = {np.nanmax(np.abs(fused - ref)):.2e}; closest reference score "
+          f"to a threshold: {dist:.2e}", flush=True)
+    for i, tgt in zip(picks, targets):
+        assert abs(ref[i] - tgt) < 1e-4, (i, ref[i], tgt)
+    bits_ref = [opt._score_to_bits(float(x)) for x in ref]
+    bits_fused = [opt._score_to_bits(float(x)) for x in fused]
+    assert bits_fused == bits_ref
+    assert sorted(set(bits_ref)) == [4, 8, 16, 32]
+    # Scores agree to the fp32 rounding of the reductions, except for the near-constant tensors
+    # (kind 2, std 1e-5 of the mean): there torch's fp32 reductions lose digits of the std, while
+    # the fused two-pass fp64 statistics match the float64 oracle.
+    other = [i for i in range(len(grads)) if i % 4 != 2]
+    near_const = [i for i in range(len(grads)) if i % 4 == 2]
+    assert np.nanmax(np.abs(fused - ref)[other]) < 1e-4
+    st = mdq_hip.grad_stats([grads[i] for i in near_const]).cpu().numpy()
+    for k, i in enumerate(near_const):
+        np.testing.assert_allclose(st[k], orc.grad_stats(grads[i].cpu().numpy()), rtol=1e-6)
+    print(f"near-constant tensors: max |score fused - score torch| {np.nanmax(np.abs(fused - ref)[near_const]):.2e}"
+          f" (torch's fp32 std), the fused statistics within 1e-6 of the float64 oracle", flush=True)
+
+
+def test_optimizer_widths_match_reference_stats_many_tensors():
+    print("case: optimizer 320 tensors fused vs reference statistics", flush=True)
+    g0 = _many_grads(12)
+    pa = [torch.nn.Parameter(torch.randn(g.shape, generator=torch.Generator().manual_seed(i)).to(DEV) * 0.02)
+          for i, g in enumerate(g0)]
+    pb = [torch.nn.Parameter(p.detach().clone()) for p in pa]
+    oa = MDQAdamWSimple(pa, block_size=128, update_freq=2, grad_stats="fused", layer_count=12, batch_size=8)
+    ob = MDQAdamWSimple(pb, block_size=128, update_freq=2, grad_stats="reference", layer_count=12, batch_size=8)
+    for t in range(1, 7):
+        gs = _many_grads(100 + t)
+        for i, (a, b) in enumerate(zip(pa, pb)):
+            a.grad = gs[i] * float(2.0 ** ((i % 9) - 4))
+            b.grad = a.grad.clone()
+        oa.step()
+        ob.step()
+        wa = [oa.state[p]["current_bit"] for p in pa]
+        wb = [ob.state[p]["current_bit"] for p in pb]
+        assert wa == wb, (t, [(i, x, y) for i, (x, y) in enumerate(zip(wa, wb)) if x != y][:5])
+        for a, b in zip(pa, pb):
+            assert torch.equal(oa.state[a]["exp_avg"], ob.state[b]["exp_avg"])
+    print(f"widths at the end: {sorted(set(wa))}", flush=True)
+    assert len(set(wa)) >= 3
