@@ -132,6 +132,31 @@ void mdq_oracle_math_chunk_digests(int which, uint32_t first, uint32_t count,
     }
 }
 
+/* The largest error, in units in the last place of the float nearest the true
+ * value, of mdq_oracle_expf (which = 0) or mdq_oracle_logf (1) over the float
+ * bit patterns first .. first+count-1, against libm's double exp / log (whose
+ * own error, below 1 double ulp, is 2^-29 of a float ulp).  Inputs whose true
+ * value is not a finite nonzero float are skipped. */
+double mdq_oracle_max_ulp_err(int which, uint32_t first, uint32_t count)
+{
+    double worst = 0.0;
+#pragma omp parallel for schedule(static, 1 << 16) reduction(max : worst)
+    for (int64_t i = 0; i < (int64_t)count; ++i) {
+        const float x = u2f(first + (uint32_t)i);
+        const double ref = which == 0 ? exp((double)x) : log((double)x);
+        const float ref32 = (float)fabs(ref);
+        if (!(ref32 > 0.0f) || isinf(ref32)) continue;
+        int e = 0;
+        (void)frexp((double)ref32, &e);
+        double ulp = ldexp(1.0, e - 24);
+        if (ulp < ldexp(1.0, -149)) ulp = ldexp(1.0, -149);
+        const float y = which == 0 ? mdq_oracle_expf(x) : mdq_oracle_logf(x);
+        const double err = fabs((double)y - ref) / ulp;
+        if (err > worst || err != err) worst = err != err ? INFINITY : err;
+    }
+    return worst;
+}
+
 /* round() of the FP64 quotient, as stquant_kernel.cu:113,123 compute it. */
 double mdq_oracle_round_div(float num, float den)
 {

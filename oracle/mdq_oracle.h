@@ -69,6 +69,9 @@ float mdq_oracle_expf(float x);
 float mdq_oracle_logf(float x);
 void mdq_oracle_expf_n(const float *x, float *y, int64_t n);
 void mdq_oracle_logf_n(const float *x, float *y, int64_t n);
+/* Max error in float ulps of mdq_oracle_expf (which 0) / mdq_oracle_logf (1)
+ * over the bit patterns first .. first+count-1, against double libm. */
+double mdq_oracle_max_ulp_err(int which, uint32_t first, uint32_t count);
 /* round((double)num / (double)den), half away from zero, as a double. */
 double mdq_oracle_round_div(float num, float den);
 void mdq_oracle_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);

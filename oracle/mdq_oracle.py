@@ -118,6 +118,8 @@ def lib():
             fn = getattr(L, name)
             fn.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64]
             fn.restype = None
+        L.mdq_oracle_max_ulp_err.argtypes = [ctypes.c_int, ctypes.c_uint32, ctypes.c_uint32]
+        L.mdq_oracle_max_ulp_err.restype = ctypes.c_double
         L.mdq_oracle_round_div.argtypes = [ctypes.c_float, ctypes.c_float]
         L.mdq_oracle_round_div.restype = ctypes.c_double
         L.mdq_oracle_philox4x32_10.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
@@ -134,6 +136,12 @@ def _ptr(a: Optional[np.ndarray]) -> Optional[int]:
         return None
     assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
     return a.ctypes.data
+
+
+def max_ulp_err(which: str, first: int, count: int) -> float:
+    """Largest error in float ulps of the oracle's exp (``which='exp'``) or log over the float bit
+    patterns ``first .. first+count-1``, against double-precision libm (all host threads)."""
+    return float(lib().mdq_oracle_max_ulp_err(0 if which == "exp" else 1, int(first), int(count)))
 
 
 def expf(x: np.ndarray) -> np.ndarray:

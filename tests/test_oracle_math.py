@@ -1,8 +1,10 @@
-"""Pins the oracle's expf/logf against float64 (numpy), and the library's host
-build of the kernel math against the oracle, bit for bit.
+"""Pins the oracle's expf/logf against float64, and the library's host build of the
+kernel math against the oracle, bit for bit.
 
 The oracle's functions stand in for CUDA expf/logf (stquant_kernel.cu:75,93).
-Bound: faithful rounding (< 1 ulp) everywhere the step evaluates them.
+Bound: faithful rounding (< 1 ulp) everywhere the step evaluates them, checked on
+every input of those ranges (mdq_oracle_max_ulp_err, against double libm) and on a
+strided sample against numpy's float64 functions.
 """
 import numpy as np
 import pytest
@@ -33,6 +35,22 @@ def test_logf_faithful_over_positive_normals(offset):
     got = orc.logf(x)
     err = _ulp_err(got, np.log(x.astype(np.float64)))
     assert err.max() < 1.0, f"max {err.max():.4f} ulp at x={x[err.argmax()]!r}"
+
+
+def test_logf_faithful_on_every_positive_normal():
+    """All 2,130,706,432 positive normal floats."""
+    err = orc.max_ulp_err("log", POS_NORMAL_LO, POS_NORMAL_HI - POS_NORMAL_LO)
+    print(f"logf: max {err:.4f} ulp over every positive normal float")
+    assert err < 1.0
+
+
+@pytest.mark.parametrize("sign", [0, 1])
+def test_expf_faithful_on_every_input_in_range(sign):
+    """Every float in [0, 88] (sign 0) and in [-87, 0] (sign 1): about 2.1e9 inputs each."""
+    hi = int(np.float32(88.0 if sign == 0 else 87.0).view(np.uint32))
+    err = orc.max_ulp_err("exp", 0x80000000 if sign else 0, hi + 1)
+    print(f"expf: max {err:.4f} ulp over every input of {'[-87, 0]' if sign else '[0, 88]'}")
+    assert err < 1.0
 
 
 def test_logf_dense_in_step_range():
