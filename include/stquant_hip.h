@@ -138,6 +138,31 @@ int stq_multi_tensor_mdq_adamw(const stq_tensor *tensors, int n_tensors,
                                int64_t *profile_cycles, int64_t profile_numel,
                                void *stream);
 
+/* Tensors per call of stq_multi_tensor_mdq_adamw_noalloc (its fixed descriptor space). */
+#define STQ_NOALLOC_MAX_TENSORS 4096
+
+/*
+ * stq_multi_tensor_mdq_adamw without any allocation, for callers that cannot
+ * allocate: loops that forbid hipMalloc / hipHostMalloc / heap allocation
+ * during a step (serving and training loops with a fixed memory plan).  No
+ * counterpart in the reference.  Same arguments and results; at most
+ * STQ_NOALLOC_MAX_TENSORS tensors per call (more: STQ_ERR_INVALID).
+ *
+ * The descriptor table lives in a fixed device array of the library
+ * (STQ_NOALLOC_MAX_TENSORS * 184 bytes = 736 KiB, held by every GPU the
+ * library runs on until the process ends) and is copied there from a static
+ * host buffer.  That copy is synchronous: the call returns after the work
+ * queued on `stream` before it has finished.  All calls on one GPU share the
+ * array: calls on the same stream are ordered, but calls on different streams
+ * of one GPU race (a later call can overwrite the table an earlier call's
+ * kernel is still reading) and must be ordered by the caller.
+ */
+int stq_multi_tensor_mdq_adamw_noalloc(const stq_tensor *tensors, int n_tensors,
+                                       int grad_dtype, int exp_avg_dtype, int exp_avg_sq_dtype,
+                                       int block_size, int rounding, uint64_t seed,
+                                       int64_t *profile_cycles, int64_t profile_numel,
+                                       void *stream);
+
 /*
  * Per-tensor gradient statistics of the MDQ bit decision, for a whole tensor
  * list: for tensor i with numel[i] elements of grad_dtype (STQ_FLOAT,

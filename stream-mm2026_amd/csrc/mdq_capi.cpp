@@ -313,11 +313,33 @@ int release_slot(Slot *s, hipStream_t stream)
     return STQ_OK;
 }
 
-// Uploads descs to a device slot on `stream` and launches.  The slot's pinned
-// staging buffer is reused only after the event recorded behind its previous
-// launch has completed.  `storage` is the code storage the kernel writes; it
-// reads `src_storage` (the same, except on a storage-changing step).
-int upload_and_launch(const std::vector<MdqDesc> &descs, int src_storage, int storage, int grad_dt, int log2b,
+// Launches the step kernel of (src_storage -> storage) over the nd
+// descriptors at dd, which the tile starts follow in the same device buffer.
+hipError_t launch_step(const MdqDesc *dd, int nd, int src, int storage, int grad_dt, int log2b, bool sr,
+                       int64_t total_tiles, unsigned long long *prof, uint64_t seed, hipStream_t stream)
+{
+    const int grid = 0;   // one workgroup per tile (total_tiles)
+    if (src == storage) {
+        switch (storage) {
+        case mdq::ST_P4: return mdq::launch_p4(dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream);
+        case mdq::ST_S8: return mdq::launch_s8(dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream);
+        case mdq::ST_S16: return mdq::launch_s16(dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream);
+        default: return mdq::launch_s32(dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream);
+        }
+    }
+    switch (storage) {
+    case mdq::ST_P4: return mdq::launch_tr_p4(src, dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream);
+    case mdq::ST_S8: return mdq::launch_tr_s8(src, dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream);
+    case mdq::ST_S16: return mdq::launch_tr_s16(src, dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream);
+    default: return mdq::launch_tr_s32(src, dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream);
+    }
+}
+
+// Uploads n descriptors to a device slot on `stream` and launches.  The slot's
+// pinned staging buffer is reused only after the event recorded behind its
+// previous launch has completed.  `storage` is the code storage the kernel
+// writes; it reads `src_storage` (the same, except on a storage-changing step).
+int upload_and_launch(const MdqDesc *descs, size_t n, int src_storage, int storage, int grad_dt, int log2b,
                       bool sr, int64_t total_tiles, unsigned long long *prof, uint64_t seed, hipStream_t stream)
 {
     int rc = refuse_capture(stream);
@@ -326,38 +348,18 @@ int upload_and_launch(const std::vector<MdqDesc> &descs, int src_storage, int st
     rc = get_ctx(&ctx);
     if (rc != STQ_OK) return rc;
     std::lock_guard<std::mutex> lk(ctx->mu);
-    const size_t n = descs.size();
     const size_t need = n * (sizeof(MdqDesc) + sizeof(long long));
     Slot *sp = nullptr;
     rc = take_slot(ctx, need, &sp);
     if (rc != STQ_OK) return rc;
     Slot &s = *sp;
-    std::memcpy(s.host, descs.data(), n * sizeof(MdqDesc));
+    std::memcpy(s.host, descs, n * sizeof(MdqDesc));
     long long *tb = reinterpret_cast<long long *>(s.host + n * sizeof(MdqDesc));
     for (size_t i = 0; i < n; ++i) tb[i] = descs[i].tile_begin;
     rc = upload(ctx, s, need, total_tiles * mdq::tile_elems(1 << log2b), stream);
     if (rc != STQ_OK) return rc;
-    hipError_t e;
-
-    const MdqDesc *dd = reinterpret_cast<const MdqDesc *>(s.dev);
-    const int nd = (int)n;
-    const int grid = 0;   // one workgroup per tile (total_tiles)
-    const int src = src_storage;
-    if (src == storage) {
-        switch (storage) {
-        case mdq::ST_P4: e = mdq::launch_p4(dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream); break;
-        case mdq::ST_S8: e = mdq::launch_s8(dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream); break;
-        case mdq::ST_S16: e = mdq::launch_s16(dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream); break;
-        default: e = mdq::launch_s32(dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream); break;
-        }
-    } else {
-        switch (storage) {
-        case mdq::ST_P4: e = mdq::launch_tr_p4(src, dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream); break;
-        case mdq::ST_S8: e = mdq::launch_tr_s8(src, dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream); break;
-        case mdq::ST_S16: e = mdq::launch_tr_s16(src, dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream); break;
-        default: e = mdq::launch_tr_s32(src, dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream); break;
-        }
-    }
+    const hipError_t e = launch_step(reinterpret_cast<const MdqDesc *>(s.dev), (int)n, src_storage, storage, grad_dt,
+                                     log2b, sr, total_tiles, prof, seed, stream);
     if (e != hipSuccess) return hip_fail(e, "kernel launch");
     return release_slot(&s, stream);
 }
@@ -429,6 +431,42 @@ int common_checks(int grad_dt, int block_size, int rounding, const int64_t *prof
     return STQ_OK;
 }
 
+// Checks the tensors of a step launch and writes the descriptors of those with
+// elements to out[0 .. *n_out) (at most cap; the caller checked n_tensors <= cap),
+// with their tile ranges; *storage is the tensors' common code storage.
+int build_step_descs(const stq_tensor *tensors, int n_tensors, int grad_dt, int ea_dt, int easq_dt, int B,
+                     MdqDesc *out, int *n_out, int *storage, int64_t *tiles_out)
+{
+    const int64_t te = mdq::tile_elems(B);
+    int st_all = -1, nd = 0;
+    int64_t tiles = 0;
+    for (int i = 0; i < n_tensors; ++i) {
+        const stq_tensor &t = tensors[i];
+        const int st = pick_storage(t.bits, ea_dt, t.exp_avg_numel, easq_dt, t.exp_avg_sq_numel, t.numel);
+        if (st < 0) return STQ_ERR_INVALID;
+        if (st_all >= 0 && st != st_all)
+            return fail(STQ_ERR_INVALID, "all tensors of one call must share the code storage");
+        st_all = st;
+        MdqDesc d;
+        const int rc = make_desc(t, st, grad_dt, B, d);
+        if (rc != STQ_OK) {
+            g_err = "tensor " + std::to_string(i) + ": " + g_err;
+            return rc;
+        }
+        if (t.numel == 0) continue;
+        d.tile_begin = tiles;
+        tiles += (t.numel + te - 1) / te;
+        d.tile_end = tiles;
+        out[nd++] = d;
+    }
+    if (tiles > 0x7fffffffLL)
+        return fail(STQ_ERR_INVALID, "too many tiles in one call (%lld); split the tensor list", (long long)tiles);
+    *n_out = nd;
+    *storage = st_all;
+    *tiles_out = tiles;
+    return STQ_OK;
+}
+
 int run(const stq_tensor *tensors, int n_tensors, int grad_dt, int ea_dt, int easq_dt, int block_size,
         int rounding, uint64_t seed, int64_t *prof, int64_t prof_numel, void *stream)
 {
@@ -438,37 +476,15 @@ int run(const stq_tensor *tensors, int n_tensors, int grad_dt, int ea_dt, int ea
     int rc = common_checks(grad_dt, block_size, rounding, prof, prof_numel, &log2b);
     if (rc != STQ_OK) return rc;
     if (n_tensors < 0 || (n_tensors > 0 && !tensors)) return fail(STQ_ERR_INVALID, "bad tensor list");
-    const int B = 1 << log2b;
-    const int64_t te = mdq::tile_elems(B);
-    std::vector<MdqDesc> descs;
-    descs.reserve((size_t)n_tensors);
-    int storage = -1;
+    std::vector<MdqDesc> descs((size_t)n_tensors);
+    int nd = 0, storage = -1;
     int64_t tiles = 0;
-    for (int i = 0; i < n_tensors; ++i) {
-        const stq_tensor &t = tensors[i];
-        const int st = pick_storage(t.bits, ea_dt, t.exp_avg_numel, easq_dt, t.exp_avg_sq_numel, t.numel);
-        if (st < 0) return STQ_ERR_INVALID;
-        if (storage >= 0 && st != storage)
-            return fail(STQ_ERR_INVALID, "all tensors of one call must share the code storage");
-        storage = st;
-        MdqDesc d;
-        rc = make_desc(t, st, grad_dt, B, d);
-        if (rc != STQ_OK) {
-            g_err = "tensor " + std::to_string(i) + ": " + g_err;
-            return rc;
-        }
-        if (t.numel == 0) continue;
-        d.tile_begin = tiles;
-        tiles += (t.numel + te - 1) / te;
-        d.tile_end = tiles;
-        descs.push_back(d);
-    }
-    if (descs.empty()) return STQ_OK;
-    if (tiles > 0x7fffffffLL)
-        return fail(STQ_ERR_INVALID, "too many tiles in one call (%lld); split the tensor list", (long long)tiles);
-    return upload_and_launch(descs, storage, storage, grad_dt, log2b, rounding == STQ_ROUND_STOCHASTIC, tiles,
-                             reinterpret_cast<unsigned long long *>(prof), seed,
-                             reinterpret_cast<hipStream_t>(stream));
+    rc = build_step_descs(tensors, n_tensors, grad_dt, ea_dt, easq_dt, 1 << log2b, descs.data(), &nd, &storage,
+                          &tiles);
+    if (rc != STQ_OK || nd == 0) return rc;
+    return upload_and_launch(descs.data(), (size_t)nd, storage, storage, grad_dt, log2b,
+                             rounding == STQ_ROUND_STOCHASTIC, tiles, reinterpret_cast<unsigned long long *>(prof),
+                             seed, reinterpret_cast<hipStream_t>(stream));
 }
 
 // The storage MDQAdamWSimple leaves a `bits`-wide tensor in after a step
@@ -558,8 +574,8 @@ int run_restore(const stq_tensor *tensors, const stq_code_out *out, int n_tensor
     if (descs.empty()) return STQ_OK;
     if (tiles > 0x7fffffffLL)
         return fail(STQ_ERR_INVALID, "too many tiles in one call (%lld); split the tensor list", (long long)tiles);
-    return upload_and_launch(descs, src, dst, grad_dt, log2b, rounding == STQ_ROUND_STOCHASTIC, tiles,
-                             reinterpret_cast<unsigned long long *>(prof), seed,
+    return upload_and_launch(descs.data(), descs.size(), src, dst, grad_dt, log2b, rounding == STQ_ROUND_STOCHASTIC,
+                             tiles, reinterpret_cast<unsigned long long *>(prof), seed,
                              reinterpret_cast<hipStream_t>(stream));
 }
 
@@ -622,7 +638,81 @@ int run_convert(const stq_code_convert *items, int n, hipStream_t stream)
 
 }  // namespace
 
+// ------------------------------------------------- allocation-free entry point
+// stq_multi_tensor_mdq_adamw_noalloc keeps its descriptor table (the MdqDesc of
+// each tensor with elements, then their int64 tile starts: the layout the step
+// kernel reads) in `scratch`, a file-scope device array that every GPU the
+// library runs on holds once, until the process ends.  It is staged on the host
+// in a static buffer, so a call allocates no device, pinned or heap memory.
+// In host code the name `scratch` stands for the host-side shadow; its device
+// address on each GPU comes from hipGetSymbolAddress (g_scratch_dev).
+constexpr size_t NOALLOC_BYTES = (size_t)STQ_NOALLOC_MAX_TENSORS * (sizeof(mdq::MdqDesc) + sizeof(long long));
+static __device__ __align__(256) char scratch[NOALLOC_BYTES];
+
+namespace {
+
+std::mutex g_noalloc_mu;                       // guards the staging buffer and g_scratch_dev
+char *g_scratch_dev[64] = {nullptr};           // scratch's device address, per device
+alignas(256) char g_noalloc_stage[NOALLOC_BYTES];
+
+int run_noalloc(const stq_tensor *tensors, int n_tensors, int grad_dt, int ea_dt, int easq_dt, int block_size,
+                int rounding, uint64_t seed, int64_t *prof, int64_t prof_numel, hipStream_t stream)
+{
+    g_err.clear();
+    if (prof_numel == 0) prof = nullptr;
+    int log2b = 0;
+    int rc = common_checks(grad_dt, block_size, rounding, prof, prof_numel, &log2b);
+    if (rc != STQ_OK) return rc;
+    if (n_tensors < 0 || (n_tensors > 0 && !tensors)) return fail(STQ_ERR_INVALID, "bad tensor list");
+    if (n_tensors > STQ_NOALLOC_MAX_TENSORS)
+        return fail(STQ_ERR_INVALID,
+                    "noalloc: %d tensors in one call, more than its fixed descriptor space holds "
+                    "(STQ_NOALLOC_MAX_TENSORS = %d); split the list or use stq_multi_tensor_mdq_adamw",
+                    n_tensors, STQ_NOALLOC_MAX_TENSORS);
+    rc = refuse_capture(stream);
+    if (rc != STQ_OK) return rc;
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+    if (dev < 0 || dev >= 64) return fail(STQ_ERR_INVALID, "device index %d out of range", dev);
+    std::lock_guard<std::mutex> lk(g_noalloc_mu);
+    MdqDesc *descs = reinterpret_cast<MdqDesc *>(g_noalloc_stage);
+    int nd = 0, storage = -1;
+    int64_t tiles = 0;
+    rc = build_step_descs(tensors, n_tensors, grad_dt, ea_dt, easq_dt, 1 << log2b, descs, &nd, &storage, &tiles);
+    if (rc != STQ_OK || nd == 0) return rc;
+    if (!g_scratch_dev[dev]) {
+        // once per device, with that device current: its copy of the array
+        void *ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+        g_scratch_dev[dev] = static_cast<char *>(ptr);
+    }
+    long long *tb = reinterpret_cast<long long *>(g_noalloc_stage + (size_t)nd * sizeof(MdqDesc));
+    for (int i = 0; i < nd; ++i) tb[i] = descs[i].tile_begin;
+    // The staging buffer is pageable memory, so the copy is synchronous: it runs after
+    // the work queued on `stream` before it (an earlier call's kernel has finished
+    // reading the table), and the buffer is free again when it returns.
+    e = hipMemcpyAsync(g_scratch_dev[dev], g_noalloc_stage, (size_t)nd * (sizeof(MdqDesc) + sizeof(long long)),
+                       hipMemcpyHostToDevice, stream);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(descriptors -> scratch)");
+    e = launch_step(reinterpret_cast<const MdqDesc *>(g_scratch_dev[dev]), nd, storage, storage, grad_dt, log2b,
+                    rounding == STQ_ROUND_STOCHASTIC, tiles, reinterpret_cast<unsigned long long *>(prof), seed,
+                    stream);
+    return e == hipSuccess ? STQ_OK : hip_fail(e, "kernel launch");
+}
+
+}  // namespace
+
 extern "C" {
+
+int stq_multi_tensor_mdq_adamw_noalloc(const stq_tensor *tensors, int n_tensors, int grad_dtype, int exp_avg_dtype,
+                                       int exp_avg_sq_dtype, int block_size, int rounding, uint64_t seed,
+                                       int64_t *profile_cycles, int64_t profile_numel, void *stream)
+{
+    return run_noalloc(tensors, n_tensors, grad_dtype, exp_avg_dtype, exp_avg_sq_dtype, block_size, rounding, seed,
+                       profile_cycles, profile_numel, reinterpret_cast<hipStream_t>(stream));
+}
 
 int stq_fused_mdq_adamw(float *p, const void *grad, int grad_dtype, int64_t grad_numel, int64_t numel,
                         void *exp_avg, int exp_avg_dtype, int64_t exp_avg_numel,

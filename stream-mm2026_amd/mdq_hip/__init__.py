@@ -15,7 +15,7 @@ import numpy as np
 import torch
 
 from . import _capi, storage
-from ._capi import ROUND_NEAREST, ROUND_STOCHASTIC, StqTensor, check, dtype_code, lib
+from ._capi import NOALLOC_MAX_TENSORS, ROUND_NEAREST, ROUND_STOCHASTIC, StqTensor, check, dtype_code, lib
 from .storage import STORE_P4, STORE_S8, STORE_S16, STORE_S32, empty_codes
 from .storage import layout_of as storage_of
 
@@ -211,17 +211,22 @@ class MultiTensorPlan:
             if v is not None:
                 self.arr[name] = v
 
-    def run(self, profile_cycles: Optional[torch.Tensor] = None) -> None:
+    def run(self, profile_cycles: Optional[torch.Tensor] = None, *, noalloc: bool = False) -> None:
+        """One launch over the plan's tensors on the current stream.  ``noalloc`` takes the
+        library's allocation-free entry point (``stq_multi_tensor_mdq_adamw_noalloc``: at
+        most NOALLOC_MAX_TENSORS tensors, the call returns once the stream's earlier work has
+        finished)."""
         if self.n == 0:
             return
         if self.device.type != "cuda":
             raise RuntimeError("p/grad must be CUDA")
         prof_ptr, prof_n = _profile_args(profile_cycles)
         gdt, eadt, easqdt = self.codes
+        L = lib()
+        fn = L.stq_multi_tensor_mdq_adamw_noalloc if noalloc else L.stq_multi_tensor_mdq_adamw
         with torch.cuda.device(self.device):
-            rc = lib().stq_multi_tensor_mdq_adamw(
-                self.arr.ctypes.data_as(ctypes.POINTER(StqTensor)), self.n, gdt, eadt, easqdt,
-                self.block_size, self.rounding, self.seed, prof_ptr, prof_n, _capi.stream_handle(self.device))
+            rc = fn(self.arr.ctypes.data_as(ctypes.POINTER(StqTensor)), self.n, gdt, eadt, easqdt,
+                    self.block_size, self.rounding, self.seed, prof_ptr, prof_n, _capi.stream_handle(self.device))
         check(rc)
 
 

@@ -15,6 +15,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libstquant_hip.so")
 
 STQ_OK, STQ_ERR_INVALID, STQ_ERR_HIP = 0, 1, 2
+NOALLOC_MAX_TENSORS = 4096        # STQ_NOALLOC_MAX_TENSORS
 ROUND_NEAREST, ROUND_STOCHASTIC = 0, 1
 
 DTYPE_CODES = {
@@ -34,6 +35,7 @@ DTYPE_CODES = {
 EXPORTED_SYMBOLS = (
     "stq_fused_mdq_adamw",
     "stq_multi_tensor_mdq_adamw",
+    "stq_multi_tensor_mdq_adamw_noalloc",
     "stq_multi_tensor_mdq_adamw_restore",
     "stq_multi_tensor_grad_stats",
     "stq_multi_tensor_convert_codes",
@@ -112,6 +114,8 @@ def lib() -> ctypes.CDLL:
     L.stq_multi_tensor_mdq_adamw.argtypes = [
         ctypes.POINTER(StqTensor), i32, i32, i32, i32, i32, i32, u64, vp, i64, vp]
     L.stq_multi_tensor_mdq_adamw.restype = ctypes.c_int
+    L.stq_multi_tensor_mdq_adamw_noalloc.argtypes = L.stq_multi_tensor_mdq_adamw.argtypes
+    L.stq_multi_tensor_mdq_adamw_noalloc.restype = ctypes.c_int
     L.stq_multi_tensor_mdq_adamw_restore.argtypes = [
         ctypes.POINTER(StqTensor), vp, i32, i32, i32, i32, i32, i32, u64, vp, i64, vp]
     L.stq_multi_tensor_mdq_adamw_restore.restype = ctypes.c_int
