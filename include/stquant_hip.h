@@ -254,7 +254,9 @@ int stq_abi_version(void);
 /*
  * Device copies of the step's fp32 math, for checking it against a CPU
  * implementation (no reference counterpart: the reference calls CUDA libm).
- *   which = 0: e^x, 1: log x (x a positive normal, +inf or NaN).
+ *   which = 0: e^x, 1: log x (x a positive normal, +inf or NaN),
+ *   3: 1 / x as the stochastic requant computes it (x a positive normal; it
+ *   must equal IEEE division).
  * stq_device_math: y[i] = f(x[i]) for device arrays x, y of n floats; or, for
  *   which = 2 (n even), the step kernel's fast v-code map: for each pair
  *   (x[2i], x[2i+1]) = (dv, vmin), dv a positive normal float,

@@ -125,7 +125,7 @@ void mdq_oracle_math_chunk_digests(int which, uint32_t first, uint32_t count,
         uint32_t hi = (c + 1 == nchunks) ? first + count : lo + chunk;
         for (uint32_t b = lo; b < hi; ++b) {
             float x = u2f(b);
-            float y = which == 0 ? mdq_oracle_expf(x) : mdq_oracle_logf(x);
+            float y = which == 0 ? mdq_oracle_expf(x) : which == 1 ? mdq_oracle_logf(x) : 1.0f / x;
             acc += mix64(((uint64_t)b << 32) | f2u(y));
         }
         digests[c] = acc;
@@ -164,17 +164,20 @@ double mdq_oracle_round_div(float num, float den)
 }
 
 /* ------------------------------------------------------------------------
- * Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as
- * easy as 1, 2, 3", SC'11): 10 rounds of the 4x32 S-P network with
+ * Philox4x32 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as easy
+ * as 1, 2, 3", SC'11): `rounds` rounds of the 4x32 S-P network with
  * multipliers 0xD2511F53 / 0xCD9E8D57 and Weyl key increments
- * 0x9E3779B9 / 0xBB67AE85.  Pinned by the Random123 known-answer vectors and
- * by rocRAND's philox4x32_10 in tests/test_oracle_philox.py.
+ * 0x9E3779B9 / 0xBB67AE85.  Ten rounds are the published default, pinned by
+ * the Random123 known-answer vectors; any round count is pinned against
+ * rocRAND's own round function (tests/test_oracle_philox.py).  Stochastic
+ * rounding draws from seven rounds (MDQO_SR_ROUNDS), the count the paper
+ * reports as passing TestU01's BigCrush.
  * ---------------------------------------------------------------------- */
-void mdq_oracle_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4])
+void mdq_oracle_philox4x32(const uint32_t ctr[4], const uint32_t key[2], int rounds, uint32_t out[4])
 {
     uint32_t c0 = ctr[0], c1 = ctr[1], c2 = ctr[2], c3 = ctr[3];
     uint32_t k0 = key[0], k1 = key[1];
-    for (int r = 0; r < 10; ++r) {
+    for (int r = 0; r < rounds; ++r) {
         if (r) { k0 += 0x9E3779B9u; k1 += 0xBB67AE85u; }
         uint64_t p0 = (uint64_t)0xD2511F53u * c0;
         uint64_t p1 = (uint64_t)0xCD9E8D57u * c2;
@@ -187,14 +190,21 @@ void mdq_oracle_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint
     out[0] = c0; out[1] = c1; out[2] = c2; out[3] = c3;
 }
 
-/* Two uniforms on the centred 2^-16 grid for element idx of a tensor. */
+void mdq_oracle_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4])
+{
+    mdq_oracle_philox4x32(ctr, key, 10, out);
+}
+
+/* Two uniforms on the centred 2^-16 grid for element idx of a tensor: word
+ * idx mod 4 of the Philox4x32 output for counter (idx / 4 low, high, tensor id,
+ * step) and key seed; its low half drives m, its high half v. */
 static inline void sr_uniforms(uint64_t idx, uint32_t tensor_id, int32_t step,
                                uint64_t seed, float *um, float *uv)
 {
     uint32_t ctr[4] = {(uint32_t)(idx >> 2), (uint32_t)(idx >> 34), tensor_id, (uint32_t)step};
     uint32_t key[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
     uint32_t out[4];
-    mdq_oracle_philox4x32_10(ctr, key, out);
+    mdq_oracle_philox4x32(ctr, key, MDQO_SR_ROUNDS, out);
     uint32_t w = out[idx & 3];
     *um = ((float)(w & 0xffffu) + 0.5f) * (1.0f / 65536.0f);
     *uv = ((float)(w >> 16) + 0.5f) * (1.0f / 65536.0f);

@@ -23,7 +23,8 @@
  * literally.
  *
  * Stochastic rounding has no reference counterpart; its definition here is
- * the one the HIP kernel implements (Philox4x32-10, Salmon et al. SC'11).
+ * the one the HIP kernel implements (seven rounds of Philox4x32, Salmon et al.
+ * SC'11).
  */
 #ifndef MDQ_ORACLE_H
 #define MDQ_ORACLE_H
@@ -75,6 +76,9 @@ double mdq_oracle_max_ulp_err(int which, uint32_t first, uint32_t count);
 /* round((double)num / (double)den), half away from zero, as a double. */
 double mdq_oracle_round_div(float num, float den);
 void mdq_oracle_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
+/* Philox4x32 with any number of rounds (the stochastic-rounding stream uses MDQO_SR_ROUNDS). */
+#define MDQO_SR_ROUNDS 7
+void mdq_oracle_philox4x32(const uint32_t ctr[4], const uint32_t key[2], int rounds, uint32_t out[4]);
 /* Order-independent 64-bit digests over the whole positive-normal range,
  * one per 2^shift-value chunk, for cross-checking another implementation
  * of the same expf / logf without materialising 2^31 outputs. */

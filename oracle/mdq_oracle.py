@@ -15,8 +15,9 @@ expf / logf            every fp32 input vs float64 exp/log, <1 ulp
                        (tests/test_oracle_math.py)
 FP64 divide + round    C ``round`` == numpy half-away rounding of the float64 quotient
                        on random and constructed-tie inputs (test_oracle_math.py)
-Philox4x32-10          Random123 known-answer vectors + rocRAND's philox4x32_10
-                       (tests/test_oracle_philox.py)
+Philox4x32            10 rounds: Random123 known-answer vectors + rocRAND's philox4x32_10;
+                       7 rounds (the stochastic-rounding stream): rocRAND's own round and
+                       key-bump functions applied 7 times (tests/test_oracle_philox.py)
 nibble pack / unpack   all 256 bytes, closed form of stquant_kernel.cu:72-74,130
 m codes / scale_m      max-|m| element -> +7 or -8 (asymmetric clamp), exact
                        ties (k+1/2)*d, codes vs a float64 closed form
@@ -124,6 +125,8 @@ def lib():
         L.mdq_oracle_round_div.restype = ctypes.c_double
         L.mdq_oracle_philox4x32_10.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
         L.mdq_oracle_philox4x32_10.restype = None
+        L.mdq_oracle_philox4x32.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+        L.mdq_oracle_philox4x32.restype = None
         L.mdq_oracle_math_chunk_digests.argtypes = [
             ctypes.c_int, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p]
         L.mdq_oracle_math_chunk_digests.restype = None
@@ -170,10 +173,22 @@ def philox4x32_10(ctr, key) -> np.ndarray:
     return out
 
 
+def philox4x32(ctr, key, rounds: int) -> np.ndarray:
+    c = np.ascontiguousarray(np.asarray(ctr, dtype=np.uint32).reshape(4))
+    k = np.ascontiguousarray(np.asarray(key, dtype=np.uint32).reshape(2))
+    out = np.zeros(4, dtype=np.uint32)
+    lib().mdq_oracle_philox4x32(_ptr(c), _ptr(k), int(rounds), _ptr(out))
+    return out
+
+
+SR_ROUNDS = 7   # MDQO_SR_ROUNDS: Philox4x32 rounds of the stochastic-rounding stream
+
+
 def math_chunk_digests(which: str, first: int, count: int, chunk: int) -> np.ndarray:
+    """Per-chunk digests of exp (``which='exp'``), log, or IEEE 1 / x (``'rcp'``) over bit patterns."""
     nchunks = (count + chunk - 1) // chunk
     out = np.zeros(nchunks, dtype=np.uint64)
-    lib().mdq_oracle_math_chunk_digests(0 if which == "exp" else 1, first, count, chunk, _ptr(out))
+    lib().mdq_oracle_math_chunk_digests({"exp": 0, "log": 1, "rcp": 3}[which], first, count, chunk, _ptr(out))
     return out
 
 

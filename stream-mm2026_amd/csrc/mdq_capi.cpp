@@ -787,7 +787,8 @@ int stq_abi_version(void) { return STQ_ABI_VERSION; }
 int stq_device_math(int which, const float *x, float *y, int64_t n, void *stream)
 {
     g_err.clear();
-    if (which < 0 || which > 2) return fail(STQ_ERR_INVALID, "which must be 0 (exp), 1 (log) or 2 (v-code map)");
+    if (which < 0 || which > 3)
+        return fail(STQ_ERR_INVALID, "which must be 0 (exp), 1 (log), 2 (v-code map) or 3 (reciprocal)");
     if (n < 0 || (n > 0 && (!x || !y)) || (which == 2 && n % 2)) return fail(STQ_ERR_INVALID, "bad arrays");
     hipError_t e = mdq::launch_math(which, x, y, n, reinterpret_cast<hipStream_t>(stream));
     return e == hipSuccess ? STQ_OK : hip_fail(e, "math kernel launch");
@@ -810,7 +811,8 @@ int stq_device_math_digests(int which, uint32_t first, uint32_t count, uint32_t 
                             void *stream)
 {
     g_err.clear();
-    if (which != 0 && which != 1) return fail(STQ_ERR_INVALID, "which must be 0 (exp) or 1 (log)");
+    if (which != 0 && which != 1 && which != 3)
+        return fail(STQ_ERR_INVALID, "which must be 0 (exp), 1 (log) or 3 (reciprocal)");
     if (chunk == 0 || chunk % 64 != 0) return fail(STQ_ERR_INVALID, "chunk must be a positive multiple of 64");
     if ((uint64_t)first + count > 0x100000000ull) return fail(STQ_ERR_INVALID, "range exceeds 2^32");
     if (count > 0 && !digests) return fail(STQ_ERR_INVALID, "null digests");

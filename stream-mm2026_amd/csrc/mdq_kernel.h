@@ -76,6 +76,23 @@ template <class T>
 __device__ __forceinline__ T ld_nt(const void *a) { return __builtin_nontemporal_load((const MDQ_GLOBAL T *)a); }
 template <class T>
 __device__ __forceinline__ void st_nt(T v, void *a) { __builtin_nontemporal_store(v, (MDQ_GLOBAL T *)a); }
+// The same streaming accesses for an address aligned only to A bytes (a view at an
+// arbitrary element offset): gfx9 global loads and stores take any alignment
+// (the compiler's unaligned-buffer-access feature of this target; it emits the
+// same single dwordx4 / dwordx2 instruction), at the cost of touching one more
+// cache line per wave instruction.
+template <class T, int A>
+__device__ __forceinline__ T ld_nt_al(const void *a)
+{
+    typedef T TA __attribute__((aligned(A)));
+    return __builtin_nontemporal_load((const MDQ_GLOBAL TA *)a);
+}
+template <class T, int A>
+__device__ __forceinline__ void st_nt_al(T v, void *a)
+{
+    typedef T TA __attribute__((aligned(A)));
+    __builtin_nontemporal_store(v, (MDQ_GLOBAL TA *)a);
+}
 template <class T>
 __device__ __forceinline__ T ld_g(const void *a) { return *(const MDQ_GLOBAL T *)a; }
 template <class T>
@@ -153,6 +170,11 @@ template <> struct GradIO<GT_F32> {
         vf4 v = ld_nt<vf4>(static_cast<const float *>(g) + i);
         o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
     }
+    // four grads at an address aligned only to the element size
+    static __device__ __forceinline__ void load4u(const void *g, int64_t i, float *o) {
+        vf4 v = ld_nt_al<vf4, 4>(static_cast<const float *>(g) + i);
+        o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+    }
     static __device__ __forceinline__ float load1(const void *g, int64_t i) {
         return ld_g<float>(static_cast<const float *>(g) + i);
     }
@@ -161,10 +183,15 @@ template <> struct GradIO<GT_F32> {
     }
 };
 template <> struct GradIO<GT_BF16> {
-    static __device__ __forceinline__ void load4(const void *g, int64_t i, float *o) {
-        vu2 v = ld_nt<vu2>(static_cast<const uint16_t *>(g) + i);
+    static __device__ __forceinline__ void unpack(vu2 v, float *o) {
         o[0] = bits_f(v.x << 16); o[1] = bits_f(v.x & 0xffff0000u);
         o[2] = bits_f(v.y << 16); o[3] = bits_f(v.y & 0xffff0000u);
+    }
+    static __device__ __forceinline__ void load4(const void *g, int64_t i, float *o) {
+        unpack(ld_nt<vu2>(static_cast<const uint16_t *>(g) + i), o);
+    }
+    static __device__ __forceinline__ void load4u(const void *g, int64_t i, float *o) {
+        unpack(ld_nt_al<vu2, 2>(static_cast<const uint16_t *>(g) + i), o);
     }
     static __device__ __forceinline__ float load1(const void *g, int64_t i) {
         return bits_f((uint32_t)ld_g<uint16_t>(static_cast<const uint16_t *>(g) + i) << 16);
@@ -177,10 +204,15 @@ template <> struct GradIO<GT_F16> {
     static __device__ __forceinline__ float h2f(uint32_t h) {
         return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
     }
-    static __device__ __forceinline__ void load4(const void *g, int64_t i, float *o) {
-        vu2 v = ld_nt<vu2>(static_cast<const uint16_t *>(g) + i);
+    static __device__ __forceinline__ void unpack(vu2 v, float *o) {
         o[0] = h2f(v.x & 0xffffu); o[1] = h2f(v.x >> 16);
         o[2] = h2f(v.y & 0xffffu); o[3] = h2f(v.y >> 16);
+    }
+    static __device__ __forceinline__ void load4(const void *g, int64_t i, float *o) {
+        unpack(ld_nt<vu2>(static_cast<const uint16_t *>(g) + i), o);
+    }
+    static __device__ __forceinline__ void load4u(const void *g, int64_t i, float *o) {
+        unpack(ld_nt_al<vu2, 2>(static_cast<const uint16_t *>(g) + i), o);
     }
     static __device__ __forceinline__ float load1(const void *g, int64_t i) {
         return h2f(ld_g<uint16_t>(static_cast<const uint16_t *>(g) + i));
@@ -474,12 +506,13 @@ __device__ __forceinline__ float dequant_m(float code, float sm, float neg8sm)
 
 // ---------------------------------------------------------------- one tile
 // Tile modes.  TILE_VECTOR: every element of the tile lies inside the tensor and
-// all pointers are 16-byte aligned, so vector accesses are used.  TILE_ELEM_PG:
+// all pointers are 16-byte aligned, so vector accesses are used.  TILE_UNALIGNED_PG:
 // the tile lies inside the tensor and the codes are aligned, but p or the grads
-// are not (views at odd element offsets of one buffer): codes move as in
-// TILE_VECTOR, p and grads one element per access, with no bounds guards.
+// are not (views at arbitrary element offsets of one buffer, as ZeRO-style flat
+// partitions hand them over): codes move as in TILE_VECTOR, and p and grads move
+// as the same 4-element vectors at element-aligned addresses.
 // TILE_GUARDED: every access element by element, guarded by idx < numel.
-enum TileMode : int { TILE_GUARDED = 0, TILE_VECTOR = 1, TILE_ELEM_PG = 2 };
+enum TileMode : int { TILE_GUARDED = 0, TILE_VECTOR = 1, TILE_UNALIGNED_PG = 2 };
 
 template <int SRC, int DST, int GT, int LOG2B, bool SR, int MODE>
 __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int lane, int wave,
@@ -491,8 +524,8 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
     constexpr bool USE_LUT = (SRC == ST_P4) && B >= 32;
     constexpr bool PAIRED = paired_codes<SRC, DST, LOG2B>();
     constexpr bool FULL = MODE != TILE_GUARDED;           // the whole tile lies inside the tensor
-    constexpr bool VEC_PG = MODE == TILE_VECTOR;          // p and grads move as 16-byte vectors
-    static_assert(MODE != TILE_ELEM_PG || C::QPL > 0, "element p/g mode needs 4-element quads");
+    constexpr bool VEC_PG = MODE == TILE_VECTOR;          // p and grads 16-byte aligned
+    static_assert(MODE != TILE_UNALIGNED_PG || C::QPL > 0, "unaligned p/g mode needs 4-element quads");
 
     unsigned long long t0 = 0;
     if (prof_on) t0 = clock64();
@@ -533,17 +566,15 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
 #pragma unroll
         for (int k = 0; k < C::QPL; ++k) {
             const uint32_t i = lbase + 4 * lane_quad<PAIRED, LOG2B>(j, k);
+            vf4 p4;
             if constexpr (VEC_PG) {
-                vf4 p4 = ld_nt<vf4>(dt.p + i);
-                pv[4 * k + 0] = p4.x; pv[4 * k + 1] = p4.y; pv[4 * k + 2] = p4.z; pv[4 * k + 3] = p4.w;
+                p4 = ld_nt<vf4>(dt.p + i);
                 GradIO<GT>::load4(dt.g, i, gv + 4 * k);
             } else {
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    pv[4 * k + c] = ld_nt<float>(dt.p + i + c);
-                    gv[4 * k + c] = GradIO<GT>::load1nt(dt.g, i + c);
-                }
+                p4 = ld_nt_al<vf4, 4>(dt.p + i);
+                GradIO<GT>::load4u(dt.g, i, gv + 4 * k);
             }
+            pv[4 * k + 0] = p4.x; pv[4 * k + 1] = p4.y; pv[4 * k + 2] = p4.z; pv[4 * k + 3] = p4.w;
             if constexpr (!(PAIRED && one_byte_codes(SRC))) CodeIO<SRC>::load4(dt, i, mc + 4 * k, vc + 4 * k);
         }
         if constexpr (PAIRED && one_byte_codes(SRC)) CodeIO<SRC>::template load8<LPB / 2>(dt, lbase, j, mc, vc);
@@ -573,7 +604,7 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
 #pragma unroll
         for (int k = 0; k < C::QPL; ++k) {
             const uint64_t q = (uint64_t)(((base + d.rng_origin) >> 2) + lane_quad<PAIRED, LOG2B>(j, k));
-            const U4 r = mdq_philox4x32_10_uk(U4{(uint32_t)q, (uint32_t)(q >> 32), d.tensor_id, d.step},
+            const U4 r = mdq_philox4x32_uk<MDQ_SR_ROUNDS>(U4{(uint32_t)q, (uint32_t)(q >> 32), d.tensor_id, d.step},
                                               (uint32_t)seed, (uint32_t)(seed >> 32));
             rw[4 * k + 0] = r.x;
             rw[4 * k + 1] = r.y;
@@ -762,7 +793,16 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
     if (!wide) {
         float qmf[EPL], qvf[EPL];
         if constexpr (SR) {
-            const float inv_dm = 1.0f / dm, inv_dv = 1.0f / dv;
+            // 1.0f / d: through mdq_rcp_rn where every lane's d lies below 2^126 (the
+            // range where it equals IEEE division), by division otherwise
+            float inv_dm, inv_dv;
+            if (__builtin_amdgcn_ballot_w64(!(dm < 0x1p126f && dv < 0x1p126f)) == 0) {
+                inv_dm = mdq_rcp_rn(dm);
+                inv_dv = mdq_rcp_rn(dv);
+            } else {
+                inv_dm = 1.0f / dm;
+                inv_dv = 1.0f / dv;
+            }
             float um[EPL], uv[EPL];
             // Philox4x32-10 per 4-element quad of the tensor: counter
             // (quad index lo, hi, tensor id, step), key = seed; word i of the
@@ -780,7 +820,7 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
                 for (int e = 0; e < EPL; ++e) {
                     const uint64_t idx = (uint64_t)(base + d.rng_origin + e);
                     const uint64_t q = idx >> 2;
-                    U4 r = mdq_philox4x32_10_uk(U4{(uint32_t)q, (uint32_t)(q >> 32), d.tensor_id, d.step},
+                    U4 r = mdq_philox4x32_uk<MDQ_SR_ROUNDS>(U4{(uint32_t)q, (uint32_t)(q >> 32), d.tensor_id, d.step},
                                                 (uint32_t)seed, (uint32_t)(seed >> 32));
                     const uint32_t w[4] = {r.x, r.y, r.z, r.w};
                     const uint32_t ww = w[idx & 3];
@@ -829,8 +869,16 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
                 }
             }
         } else {
-            const float hdm = 0.5f * dm, hdv = 0.5f * dv;
-            const float ilm = mdq_inv_lo(__builtin_amdgcn_rcpf(dm));
+            // A block whose m scale is 2^126 or more (1- or 2-bit codes of |m| near FLT_MAX)
+            // has a subnormal reciprocal, which the roundings below cannot use.  There m and
+            // dm are both scaled by 2^-64 (msc), exact wherever the code depends on it (a
+            // quotient at or above 1/2 needs |m| >= dm / 2 >= 2^125), and every element of
+            // the block takes the exact rounding.
+            const bool bigm = dm >= 0x1p126f;
+            const float msc = bigm ? 0x1p-64f : 1.0f;
+            const float dmq = dm * msc;
+            const float hdm = 0.5f * dmq, hdv = 0.5f * dv;
+            const float ilm = mdq_inv_lo(__builtin_amdgcn_rcpf(dmq));
             const float ilv = mdq_inv_lo(__builtin_amdgcn_rcpf(dv));
             if (fastv) {
                 // The exact code is K = round-half-away(u / dv), u = fl(log x - vmin).
@@ -857,7 +905,7 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
                                  1.001f;
                 const float near = 0.5f - ep;
                 const float rdm = __builtin_amdgcn_rcpf(dm);
-                const float nearm = 0.5f - fma_(d.qm, 6.0e-7f, 6.0e-7f);
+                const float nearm = bigm ? -1.0f : 0.5f - fma_(d.qm, 6.0e-7f, 6.0e-7f);
                 bool redo[EPL], redo_m[EPL];
                 bool any = false;
 #pragma unroll
@@ -875,7 +923,8 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
                 if (__builtin_amdgcn_ballot_w64(any)) {
 #pragma unroll
                     for (int e = 0; e < EPL; ++e) {
-                        if (redo_m[e]) qmf[e] = __builtin_copysignf(mdq_round_half_away(fabsf(m[e]), dm, ilm, hdm), m[e]);
+                        if (redo_m[e])
+                            qmf[e] = __builtin_copysignf(mdq_round_half_away(fabsf(m[e]) * msc, dmq, ilm, hdm), m[e]);
                         if (redo[e]) qvf[e] = mdq_round_half_away(mdq_logf(v[e] + 1e-12f) - s_vmin, dv, ilv, hdv);
                     }
                 }
@@ -886,11 +935,18 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
                 // as well (:113-127).  The fast path runs only when every v, and so every
                 // m and both scales, is finite.
                 const bool sm_fin = dm <= __FLT_MAX__, sv_fin = dv <= __FLT_MAX__;
+                float K[EPL];
+                if (__builtin_amdgcn_ballot_w64(bigm)) {
+#pragma unroll
+                    for (int e = 0; e < EPL; ++e) K[e] = mdq_round_half_away(fabsf(m[e]) * msc, dmq, ilm, hdm);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < EPL; ++e) K[e] = mdq_round_half_away(fabsf(m[e]), dm, ilm, hdm);
+                }
 #pragma unroll
                 for (int e = 0; e < EPL; ++e) {
-                    const float K = mdq_round_half_away(fabsf(m[e]), dm, ilm, hdm);
                     const float u = lv[e] - s_vmin;
-                    qmf[e] = sm_fin && fabsf(m[e]) <= __FLT_MAX__ ? __builtin_copysignf(K, m[e]) : 0.0f;
+                    qmf[e] = sm_fin && fabsf(m[e]) <= __FLT_MAX__ ? __builtin_copysignf(K[e], m[e]) : 0.0f;
                     qvf[e] = sv_fin && u <= __FLT_MAX__ ? mdq_round_half_away(u, dv, ilv, hdv) : 0.0f;
                 }
             }
@@ -945,13 +1001,9 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
                 if constexpr (DST == ST_P4) CodeIO<DST>::store4f(ot, i, pk + 4 * k);
                 else CodeIO<DST>::store4(ot, i, qmi + 4 * k, qvi + 4 * k);
             }
-            if constexpr (VEC_PG) {
-                vf4 o = {pv[4 * k + 0], pv[4 * k + 1], pv[4 * k + 2], pv[4 * k + 3]};
-                st_nt<vf4>(o, dt.p + i);
-            } else {
-#pragma unroll
-                for (int c = 0; c < 4; ++c) st_nt<float>(pv[4 * k + c], dt.p + i + c);
-            }
+            const vf4 o = {pv[4 * k + 0], pv[4 * k + 1], pv[4 * k + 2], pv[4 * k + 3]};
+            if constexpr (VEC_PG) st_nt<vf4>(o, dt.p + i);
+            else st_nt_al<vf4, 4>(o, dt.p + i);
         }
         if constexpr (PAIRED && one_byte_codes(DST)) {
             if constexpr (DST == ST_P4) CodeIO<DST>::template store8f<LPB / 2>(ot, lbase, j, pk);
@@ -1025,7 +1077,7 @@ __global__ __launch_bounds__(Cfg<LOG2B>::THREADS) void mdq_step_kernel(const Mdq
         mdq_step_tile<SRC, DST, GT, LOG2B, SR, TILE_VECTOR>(d, tl, lane, wave, lut_s, xw_s, seed, prof_on, pa);
     } else if (C::QPL > 0 && inside && (d.flags & DF_CODES_ALIGNED)) {
         if constexpr (C::QPL > 0)
-            mdq_step_tile<SRC, DST, GT, LOG2B, SR, TILE_ELEM_PG>(d, tl, lane, wave, lut_s, xw_s, seed, prof_on, pa);
+            mdq_step_tile<SRC, DST, GT, LOG2B, SR, TILE_UNALIGNED_PG>(d, tl, lane, wave, lut_s, xw_s, seed, prof_on, pa);
     } else {
         mdq_step_tile<SRC, DST, GT, LOG2B, SR, TILE_GUARDED>(d, tl, lane, wave, lut_s, xw_s, seed, prof_on, pa);
     }

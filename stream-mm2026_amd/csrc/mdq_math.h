@@ -14,7 +14,11 @@
 // * mdq_round_half_away: round(u / d) for u >= 0 with ties away from zero,
 //   exactly as round((double)u / (double)d) (stquant_kernel.cu:113,123)
 //   evaluates for quotients below 2^19, using one fp32 fma residual.
-// * mdq_philox4x32_10: Philox4x32-10 (Salmon et al., SC'11).
+// * mdq_philox4x32<R>: R rounds of Philox4x32 (Salmon et al., SC'11); R = 10 is
+//   the published default, and stochastic rounding uses R = 7 (MDQ_SR_ROUNDS),
+//   the round count the paper reports as passing TestU01's BigCrush.
+// * mdq_rcp_rn: 1 / d correctly rounded, from the hardware reciprocal and one
+//   fma Newton step.
 #pragma once
 #include <stdint.h>
 
@@ -165,10 +169,14 @@ MDQ_HD float mdq_inv_lo(float inv_d_within_1ulp) { return bits_f(f_bits(inv_d_wi
 
 struct U4 { uint32_t x, y, z, w; };
 
-MDQ_HD U4 mdq_philox4x32_10(U4 c, uint32_t k0, uint32_t k1)
+// Philox4x32 rounds of the stochastic-rounding stream.
+#define MDQ_SR_ROUNDS 7
+
+template <int R>
+MDQ_HD U4 mdq_philox4x32(U4 c, uint32_t k0, uint32_t k1)
 {
 #pragma unroll
-    for (int r = 0; r < 10; ++r) {
+    for (int r = 0; r < R; ++r) {
         if (r) { k0 += 0x9E3779B9u; k1 += 0xBB67AE85u; }
         uint64_t p0 = (uint64_t)0xD2511F53u * c.x;
         uint64_t p1 = (uint64_t)0xCD9E8D57u * c.z;
@@ -181,6 +189,8 @@ MDQ_HD U4 mdq_philox4x32_10(U4 c, uint32_t k0, uint32_t k1)
     }
     return c;
 }
+
+MDQ_HD U4 mdq_philox4x32_10(U4 c, uint32_t k0, uint32_t k1) { return mdq_philox4x32<10>(c, k0, k1); }
 
 #if defined(__HIPCC__)
 // a ^ b ^ k as one v_bitop3_b32 (truth table 0x96, the three-input XOR), which
@@ -197,11 +207,12 @@ __device__ __forceinline__ uint32_t xor3_uk(uint32_t a, uint32_t b, uint32_t k)
 #endif
 }
 
-// mdq_philox4x32_10 for a wave-uniform key (the step kernel's seed), same
+// mdq_philox4x32<R> for a wave-uniform key (the step kernel's seed), same
 // result.  Round 0 keeps the plain XORs (its tensor-id and step words are
-// uniform too, so the compiler folds them in scalar registers); the other nine
+// uniform too, so the compiler folds them in scalar registers); the other
 // rounds fuse each output word's two XORs.
-__device__ __forceinline__ U4 mdq_philox4x32_10_uk(U4 c, uint32_t k0, uint32_t k1)
+template <int R>
+__device__ __forceinline__ U4 mdq_philox4x32_uk(U4 c, uint32_t k0, uint32_t k1)
 {
     {
         const uint64_t p0 = (uint64_t)0xD2511F53u * c.x;
@@ -209,7 +220,7 @@ __device__ __forceinline__ U4 mdq_philox4x32_10_uk(U4 c, uint32_t k0, uint32_t k
         c = U4{(uint32_t)(p1 >> 32) ^ c.y ^ k0, (uint32_t)p1, (uint32_t)(p0 >> 32) ^ c.w ^ k1, (uint32_t)p0};
     }
 #pragma unroll
-    for (int r = 1; r < 10; ++r) {
+    for (int r = 1; r < R; ++r) {
         k0 += 0x9E3779B9u;
         k1 += 0xBB67AE85u;
         const uint64_t p0 = (uint64_t)0xD2511F53u * c.x;
@@ -222,6 +233,24 @@ __device__ __forceinline__ U4 mdq_philox4x32_10_uk(U4 c, uint32_t k0, uint32_t k
 #endif
 
 // Uniforms on the centred 2^-16 grid: (k + 1/2) / 65536, k in [0, 65535].
-MDQ_HD float mdq_u16_uniform(uint32_t k16) { return ((float)k16 + 0.5f) * (1.0f / 65536.0f); }
+// (k16 + 0.5) / 2^16 as k16 * 2^-16 + 2^-17: both terms and the sum are exact
+// (17 significant bits), so the one fma equals the add-then-multiply form.
+MDQ_HD float mdq_u16_uniform(uint32_t k16) { return fma_((float)k16, 1.0f / 65536.0f, 1.0f / 131072.0f); }
+
+// 1 / d correctly rounded for a positive normal d below 2^126 (where 1 / d is a
+// normal float).  On the device: the hardware reciprocal r (within 1 ulp) and
+// one Newton step r + r (1 - d r) with an fma residual; equal to IEEE 1.0f / d
+// for every float of that range, and for no larger d (checked exhaustively
+// against the oracle's division, stq_device_math_digests).  The host build
+// divides.
+MDQ_HD float mdq_rcp_rn(float d)
+{
+#if defined(__HIP_DEVICE_COMPILE__)
+    const float r = __builtin_amdgcn_rcpf(d);
+    return fma_(r, fma_(-d, r, 1.0f), r);
+#else
+    return 1.0f / d;
+#endif
+}
 
 }  // namespace mdq

@@ -7,9 +7,10 @@
 
 namespace mdq {
 
+// which: 0 e^x, 1 log x, 3 the correctly rounded reciprocal of the stochastic requant
 __device__ __forceinline__ float eval_math(int which, float x)
 {
-    return which == 0 ? mdq_expf(x) : mdq_logf(x);
+    return which == 0 ? mdq_expf(x) : which == 1 ? mdq_logf(x) : mdq_rcp_rn(x);
 }
 
 __global__ __launch_bounds__(256) void math_kernel(int which, const float *__restrict__ x,

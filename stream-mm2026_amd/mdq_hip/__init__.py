@@ -432,12 +432,12 @@ def device_log_approx_error(first: int, count: int, slope: float = 0.0, device="
 
 
 def device_math(which: str, x: torch.Tensor) -> torch.Tensor:
-    """Device e^x (``which='exp'``) or log x (``'log'``) with the kernels' own fp32 code; or
-    ``'vcode_map'``: x holds (dv, vmin) pairs, the result the fast v-code path's
-    (ln 2 / dv, -vmin / dv) pairs."""
+    """Device e^x (``which='exp'``), log x (``'log'``) or the stochastic requant's reciprocal
+    (``'rcp'``) with the kernels' own fp32 code; or ``'vcode_map'``: x holds (dv, vmin) pairs,
+    the result the fast v-code path's (ln 2 / dv, -vmin / dv) pairs."""
     assert x.is_cuda and x.dtype == torch.float32 and x.is_contiguous()
     y = torch.empty_like(x)
-    code = {"exp": 0, "log": 1, "vcode_map": 2}[which]
+    code = {"exp": 0, "log": 1, "vcode_map": 2, "rcp": 3}[which]
     with torch.cuda.device(x.device):
         check(lib().stq_device_math(code, _ptr(x), _ptr(y), x.numel(), _capi.stream_handle(x.device)))
     return y
@@ -448,7 +448,7 @@ def device_math_digests(which: str, first: int, count: int, chunk: int, device=N
     nchunks = (count + chunk - 1) // chunk
     dig = torch.zeros(nchunks, dtype=torch.int64, device=device)
     with torch.cuda.device(device):
-        check(lib().stq_device_math_digests(0 if which == "exp" else 1, first, count, chunk,
+        check(lib().stq_device_math_digests({"exp": 0, "log": 1, "rcp": 3}[which], first, count, chunk,
                                             dig.data_ptr(), _capi.stream_handle(device)))
     return dig
 

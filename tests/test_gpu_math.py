@@ -1,7 +1,8 @@
 """The kernels' own exp/log (mdq_math.h, device build) against the oracle's
 C implementation: bit-identical on every input of their domain, checked via
 per-chunk digests over all 2^31 - 2^23 positive normals (log) and all 2^32
-bit patterns (exp), plus an elementwise pass."""
+bit patterns (exp), plus an elementwise pass.  The stochastic requant's
+reciprocal (mdq_rcp_rn) against IEEE division on every positive normal below 2^126."""
 import os
 import re
 
@@ -33,6 +34,9 @@ def test_device_math_elementwise():
     ("log", 0x00800000, 0x7F800000 - 0x00800000 + 1),      # positive normals and +inf
     ("exp", 0, 1 << 31),
     ("exp", 1 << 31, (1 << 31) - 1),
+    # the stochastic requant's 1 / d (hardware reciprocal + one Newton step) against the
+    # oracle's IEEE division, every positive normal d below 2^126 (the kernel divides above)
+    ("rcp", 0x00800000, 0x7E800000 - 0x00800000),
 ])
 def test_device_math_exhaustive_digests(which, first, count):
     chunk = 1 << 22

@@ -53,7 +53,9 @@ class NonfiniteCase(Case):
         got = self.tp.cpu().numpy()
         nan_g, nan_a = np.isnan(got), np.isnan(self.p)
         assert np.array_equal(nan_g, nan_a), f"params: NaN at {np.nonzero(nan_g != nan_a)[0][:5]} differs"
-        fin = ~nan_a
+        inf_a = np.isinf(self.p)
+        assert np.array_equal(got[inf_a], self.p[inf_a]), "params: infinities differ"
+        fin = np.isfinite(self.p)
         assert_params_close(self.tp[torch.from_numpy(fin).to(self.tp.device)], self.p[fin], p_prev[fin])
         resync_params(self.tp, self.p)
 
@@ -170,4 +172,35 @@ def test_exp_argument_range_edges(storage, bits, B):
         p_prev = c.p.copy()
         c.oracle_step(g, step, bits)
         mdq_hip.multi_tensor_step([c.entry(tg, step, bits)], B)
+        c.check(p_prev)
+
+
+@pytest.mark.parametrize("rounding", [orc.ROUND_NEAREST, orc.ROUND_STOCHASTIC])
+def test_huge_m_scales(rounding):
+    """Blocks whose new m scale reaches 2^126 and beyond (1-bit codes dequantised with scales
+    near 3e37), in the same waves as ordinary blocks: the stochastic requant's 1 / scale leaves
+    its fast reciprocal, exact only below 2^126, for IEEE division there.  Two steps, against
+    the oracle."""
+    print(f"case: huge m scales rounding={rounding}", flush=True)
+    B, bits = 128, 1
+    rng = np.random.default_rng(91)
+    c = NonfiniteCase(B * 4 * 6, B, orc.STORE_S8, rng)
+    cm, cv, sm, sv, vm = c.state
+    nb = sm.size
+    cm[:] = rng.integers(-4, 5, cm.size, dtype=np.int8)
+    cv[:] = rng.integers(0, 2, cv.size, dtype=np.uint8)
+    sm[:] = np.float32(1e-4)
+    sv[:] = np.float32(1.0)
+    vm[:] = np.float32(-20.0)
+    big = rng.choice(nb, nb // 3, replace=False)
+    sm[big] = (10.0 ** rng.uniform(37.2, 37.6, big.size)).astype(np.float32)   # |m| up to 1.6e38
+    for a, t in ((cm, c.tcm), (cv, c.tcv), (sm, c.tsm), (sv, c.tsv), (vm, c.tvm)):
+        t.copy_(torch.from_numpy(a.copy()))
+    for step in (1, 2):
+        g, tg = Case.grads(c, rng)
+        p_prev = c.p.copy()
+        c.oracle_step(g, step, bits, rounding=rounding, seed=3)
+        assert float(np.max(sm)) >= 2.0 ** 126                    # the range the guard covers
+        mdq_hip.multi_tensor_step([c.entry(tg, step, bits)], B,
+                                  rounding="stochastic" if rounding else "nearest", seed=3)
         c.check(p_prev)
