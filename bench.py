@@ -447,6 +447,105 @@ def cpu_baseline(gdt: str, bits: int, B: int, seconds: float, rounding: str = "n
                        f"1 thread: {steps1} steps, {el1:.1f} s")
 
 
+# ---------------------------------------------------------------------------------------------
+# rocprofv3 summaries (the figures under profiles/ are made by these functions from the CSV files
+# rocprofv3 writes; nothing is copied by hand)
+# ---------------------------------------------------------------------------------------------
+def _csv_rows(d, suffix):
+    import csv
+    import glob
+    rows = []
+    for f in sorted(glob.glob(os.path.join(d, "**", f"*{suffix}"), recursive=True)):
+        with open(f, newline="") as fh:
+            rows.extend(csv.DictReader(fh))
+    if not rows:
+        raise SystemExit(f"bench.py: no *{suffix} under {d}")
+    return rows
+
+
+def _dispatch_key(r):
+    return int(r.get("Dispatch_Id") or r.get("Correlation_Id") or 0)
+
+
+def trace_stats(trace_dir, kernel, skip):
+    """Kernel durations (ns) of the dispatches whose name contains ``kernel``, in dispatch order,
+    the first ``skip`` (warm-up launches) dropped."""
+    rows = [r for r in _csv_rows(trace_dir, "kernel_trace.csv") if kernel in r["Kernel_Name"]]
+    rows.sort(key=_dispatch_key)
+    durs = [int(r["End_Timestamp"]) - int(r["Start_Timestamp"]) for r in rows]
+    timed = durs[skip:]
+    if not timed:
+        raise SystemExit(f"bench.py: {len(durs)} dispatches of {kernel!r}, none left after skipping {skip}")
+    return dict(name=rows[0]["Kernel_Name"], dispatches=len(durs), skipped=skip, timed=len(timed),
+                avg_ns=sum(timed) / len(timed), min_ns=min(timed), max_ns=max(timed),
+                all_avg_ns=sum(durs) / len(durs))
+
+
+def counter_means(pmc_dir, kernel):
+    """Mean per dispatch of each counter over the dispatches whose name contains ``kernel``."""
+    acc = {}
+    for r in _csv_rows(pmc_dir, "counter_collection.csv"):
+        if kernel in r["Kernel_Name"]:
+            acc.setdefault(r["Counter_Name"], {}).setdefault(_dispatch_key(r), 0.0)
+            acc[r["Counter_Name"]][_dispatch_key(r)] += float(r["Counter_Value"])
+    return {c: sum(v.values()) / len(v) for c, v in acc.items()}
+
+
+def profile_summary(args):
+    """Writes ``<out>.json`` and ``<out>.md`` from rocprofv3 runs of this script: a kernel trace
+    (``--trace``), and optionally FETCH_SIZE / WRITE_SIZE runs (``--fetch`` / ``--write``) made
+    with ``--copy-gib`` so the plain copy's counters calibrate them, and an SQ counter run."""
+    shapes_fn, gdt, cfg_bits, B = CONFIGS[args.config]
+    bits = cfg_bits if args.bits is None else args.bits
+    N = sum(n for _, n in shapes_fn())
+    alg = bytes_per_param(2 if gdt == "bf16" else 4, bits, B) * N
+    t = trace_stats(args.trace, args.kernel, args.skip)
+    out = dict(kernel=t["name"], workload=f"{args.config}, {bits}-bit codes, B={B}, {gdt} grads, "
+                                            f"{args.rounding} rounding", params=N,
+               dispatches=t["dispatches"], warmup_dispatches_dropped=t["skipped"], calls=t["timed"],
+               avg_ns=t["avg_ns"], min_ns=t["min_ns"], max_ns=t["max_ns"], avg_ns_with_warmup=t["all_avg_ns"],
+               algorithmic_bytes=alg, achieved_gbs=alg / t["avg_ns"], frac_of_peak=alg / t["avg_ns"] / HBM_PEAK_GBS)
+    if args.fetch and args.write:
+        fk, fc = counter_means(args.fetch, args.kernel), counter_means(args.fetch, "copyBuffer")
+        wk, wc = counter_means(args.write, args.kernel), counter_means(args.write, "copyBuffer")
+        copy_kib = args.copy_gib * (1 << 30) / 1024.0
+        fs, ws = copy_kib / fc["FETCH_SIZE"], copy_kib / wc["WRITE_SIZE"]
+        traffic = (fk["FETCH_SIZE"] * fs + wk["WRITE_SIZE"] * ws) * 1024.0
+        out.update(fetch_kib_per_dispatch=fk["FETCH_SIZE"], write_kib_per_dispatch=wk["WRITE_SIZE"],
+                   copy_fetch_kib=fc["FETCH_SIZE"], copy_write_kib=wc["WRITE_SIZE"], fetch_scale=fs, write_scale=ws,
+                   traffic_bytes=traffic, traffic_over_algorithmic=traffic / alg)
+    if args.sq:
+        sq = counter_means(args.sq, args.kernel)
+        if "SQ_WAVES" in sq and "SQ_INSTS_VALU" in sq:
+            sq["VALU_insts_per_wave"] = sq["SQ_INSTS_VALU"] / sq["SQ_WAVES"]
+        out["sq"] = sq
+    with open(args.profile_summary + ".json", "w") as f:
+        json.dump(out, f, indent=1)
+    md = [f"# rocprofv3: `{t['name'][:90]}`", "", f"Workload: {out['workload']}, {N:,} params.", "",
+          "Commands (run from /tmp with TMPDIR=/tmp on one MI355X; `$GRAFT_REPO_ROOT` = the repo root):", ""]
+    md += [f"    {c}" for c in args.cmd] + [""]
+    md += ["## Kernel time (kernel trace, warm-up launches dropped)", "",
+           f"{t['dispatches']} dispatches, the first {t['skipped']} (warm-up) dropped: average over the "
+           f"{t['timed']} timed launches **{t['avg_ns'] / 1e6:.3f} ms** (min {t['min_ns'] / 1e6:.3f}, max "
+           f"{t['max_ns'] / 1e6:.3f}; {t['all_avg_ns'] / 1e6:.3f} with the warm-up).", "",
+           f"Algorithmic bytes per launch {alg:,.0f} -> {out['achieved_gbs']:,.0f} GB/s = "
+           f"**{100 * out['frac_of_peak']:.1f} %** of 8 TB/s.", ""]
+    if "traffic_bytes" in out:
+        md += ["## HBM traffic (FETCH_SIZE / WRITE_SIZE, KiB per dispatch)", "",
+               "| | kernel | copy of known size | scale (copy bytes / copy reading) |", "|---|---|---|---|",
+               f"| FETCH_SIZE | {out['fetch_kib_per_dispatch']:,.0f} | {out['copy_fetch_kib']:,.0f} | "
+               f"{out['fetch_scale']:.4f} |",
+               f"| WRITE_SIZE | {out['write_kib_per_dispatch']:,.0f} | {out['copy_write_kib']:,.0f} | "
+               f"{out['write_scale']:.4f} |", "",
+               f"Scaled traffic {out['traffic_bytes']:,.0f} B per launch = "
+               f"{out['traffic_over_algorithmic']:.4f} x the algorithmic bytes.", ""]
+    if "sq" in out:
+        md += ["## SQ counters (per dispatch)", ""] + [f"- {k}: {v:.4g}" for k, v in sorted(out["sq"].items())] + [""]
+    with open(args.profile_summary + ".md", "w") as f:
+        f.write("\n".join(md))
+    print(json.dumps(out))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -478,7 +577,19 @@ def main():
     ap.add_argument("--shard-rank", type=int, default=0, help="which share --shard-of times")
     ap.add_argument("--copy-gib", type=float, default=0.0,
                     help="also run a plain device-to-device copy of this many GiB (rocprof calibration)")
+    ap.add_argument("--profile-summary", metavar="OUT", default=None,
+                    help="write OUT.json / OUT.md from rocprofv3 output directories (no GPU work)")
+    ap.add_argument("--trace", help="with --profile-summary: rocprofv3 --kernel-trace output directory")
+    ap.add_argument("--fetch", help="with --profile-summary: rocprofv3 --pmc FETCH_SIZE output directory")
+    ap.add_argument("--write", help="with --profile-summary: rocprofv3 --pmc WRITE_SIZE output directory")
+    ap.add_argument("--sq", help="with --profile-summary: rocprofv3 --pmc SQ_* output directory")
+    ap.add_argument("--kernel", default="mdq_step_kernel", help="with --profile-summary: kernel name substring")
+    ap.add_argument("--skip", type=int, default=0, help="with --profile-summary: warm-up dispatches to drop")
+    ap.add_argument("--cmd", action="append", default=[], help="with --profile-summary: a command to record")
     args = ap.parse_args()
+    if args.profile_summary:
+        profile_summary(args)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the step shards by quant block across GPUs "
               "with no communication inside the step; --shard-of N times one GPU's share); run with "
@@ -567,8 +678,9 @@ def main():
     # HBM bytes per launch measured by rocprofv3 (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0,
     # the factors that map a plain 4 GiB copy's counters to 4 GiB), committed under profiles/
     traffic, traffic_src = None, None
-    prof_json = os.path.join(ROOT, "profiles", f"mdq_step_{args.config}_{w['gdt']}_{STORAGE_NAMES[w['bits']]}_b{w['B']}.json")
-    if os.path.exists(prof_json) and shard is None:
+    prof_json = os.path.join(ROOT, "profiles", f"mdq_step_{args.config}_{w['gdt']}_{STORAGE_NAMES[w['bits']]}_b{w['B']}"
+                             f"{'_stochastic' if args.rounding == 'stochastic' else ''}.json")
+    if os.path.exists(prof_json) and shard is None and "traffic_bytes" in open(prof_json).read():
         with open(prof_json) as f:
             traffic = json.load(f)["traffic_bytes"]
         traffic_src = os.path.relpath(prof_json, ROOT)
