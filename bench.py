@@ -174,8 +174,10 @@ def build_workload(name, dev, seed=0, bits=None):
 ALIGN_ELEMS = 256
 
 
-def sweep_config5(dev, steps: int, warmup: int, packed_views: bool = False):
-    """Config 5 over {4, 8}-bit x B {64, 128, 256} x {nearest, stochastic}: ms/step, GB/s, params/s."""
+def sweep_config5(dev, steps: int, warmup: int, packed_views: bool = False, view_align: int = 1):
+    """Config 5 over {4, 8}-bit x B {64, 128, 256} x {nearest, stochastic}: ms/step, GB/s, params/s.
+    ``packed_views``: params and grads as views of one buffer, each tensor starting at the next
+    multiple of ``view_align`` elements after the previous one (1: back to back)."""
     import torch
 
     import mdq_hip
@@ -194,7 +196,7 @@ def sweep_config5(dev, steps: int, warmup: int, packed_views: bool = False):
         NP = offs[-1]
         offs_pg = [0]
         for n in sizes:
-            offs_pg.append(offs_pg[-1] + n)
+            offs_pg.append((offs_pg[-1] + n + view_align - 1) // view_align * view_align)
         if not packed_views:
             offs_pg = offs
         p = torch.empty(NP, dtype=torch.float32, device=dev).normal_(0.0, 0.02, generator=gen)
@@ -246,7 +248,8 @@ def sweep_config5(dev, steps: int, warmup: int, packed_views: bool = False):
             del cm, cv, sm, sv, vm, entries, plan
         del p, g
         torch.cuda.empty_cache()
-    return dict(params=N, tensors=len(sizes), packed_views=packed_views, points=points)
+    return dict(params=N, tensors=len(sizes), packed_views=packed_views,
+                view_align=view_align if packed_views else ALIGN_ELEMS, points=points)
 
 
 def e2e_gpt2(steps: int, warmup: int, out_path):
@@ -481,14 +484,21 @@ def trace_stats(trace_dir, kernel, skip):
                 all_avg_ns=sum(durs) / len(durs))
 
 
-def counter_means(pmc_dir, kernel):
-    """Mean per dispatch of each counter over the dispatches whose name contains ``kernel``."""
+def counter_means(pmc_dir, kernel, last=None):
+    """Mean per dispatch of each counter over the dispatches whose name contains ``kernel`` (only
+    the ``last`` of them in dispatch order, when given)."""
     acc = {}
     for r in _csv_rows(pmc_dir, "counter_collection.csv"):
         if kernel in r["Kernel_Name"]:
             acc.setdefault(r["Counter_Name"], {}).setdefault(_dispatch_key(r), 0.0)
             acc[r["Counter_Name"]][_dispatch_key(r)] += float(r["Counter_Value"])
-    return {c: sum(v.values()) / len(v) for c, v in acc.items()}
+    out = {}
+    for c, v in acc.items():
+        vals = [v[k] for k in sorted(v)]
+        if last:
+            vals = vals[-last:]
+        out[c] = sum(vals) / len(vals)
+    return out
 
 
 def profile_summary(args):
@@ -506,8 +516,9 @@ def profile_summary(args):
                avg_ns=t["avg_ns"], min_ns=t["min_ns"], max_ns=t["max_ns"], avg_ns_with_warmup=t["all_avg_ns"],
                algorithmic_bytes=alg, achieved_gbs=alg / t["avg_ns"], frac_of_peak=alg / t["avg_ns"] / HBM_PEAK_GBS)
     if args.fetch and args.write:
-        fk, fc = counter_means(args.fetch, args.kernel), counter_means(args.fetch, "copyBuffer")
-        wk, wc = counter_means(args.write, args.kernel), counter_means(args.write, "copyBuffer")
+        # the calibration copies are the last three copy dispatches (the workload's set-up may copy too)
+        fk, fc = counter_means(args.fetch, args.kernel), counter_means(args.fetch, "copyBuffer", last=3)
+        wk, wc = counter_means(args.write, args.kernel), counter_means(args.write, "copyBuffer", last=3)
         copy_kib = args.copy_gib * (1 << 30) / 1024.0
         fs, ws = copy_kib / fc["FETCH_SIZE"], copy_kib / wc["WRITE_SIZE"]
         traffic = (fk["FETCH_SIZE"] * fs + wk["WRITE_SIZE"] * ws) * 1024.0
@@ -563,6 +574,9 @@ def main():
                     help="time BASELINE config 5 over bits x block x rounding (one JSON line with all points)")
     ap.add_argument("--packed-views", action="store_true",
                     help="with --sweep-config5: params and grads as views packed back to back (odd offsets)")
+    ap.add_argument("--view-align", type=int, default=1,
+                    help="with --packed-views: each tensor's params and grads start on a multiple of this "
+                         "many elements")
     ap.add_argument("--e2e-gpt2", action="store_true",
                     help="BASELINE config 3: GPT-2 small pretraining, stochastic vs nearest vs AdamW")
     ap.add_argument("--e2e-steps", type=int, default=300)
@@ -601,7 +615,8 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     if args.sweep_config5:
-        res = sweep_config5(dev, args.steps, args.warmup, packed_views=args.packed_views)
+        res = sweep_config5(dev, args.steps, args.warmup, packed_views=args.packed_views,
+                            view_align=max(1, args.view_align))
         print(json.dumps({"metric": "config 5 sweep: params/s and HBM GB/s per point", "n_gpus": 1,
                           "steps": args.steps, "warmup": args.warmup, "data": "synthetic", **res}), flush=True)
         return
