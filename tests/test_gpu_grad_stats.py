@@ -159,6 +159,40 @@ def test_nonfinite_patterns_match_torch_on_the_gpu(case):
     assert np.array_equal(np.isnan(got), np.isnan(ref)) and np.array_equal(np.isinf(got), np.isinf(ref)), (got, ref)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_tiny_constant_and_offset_values(dtype):
+    """Full tiles whose per-group fp32 moments the kernel must not trust: grads so small that
+    squared deviations underflow fp32 (redone in fp64), constant and all-zero tiles, a large
+    offset with a tiny spread, values next to FLT_MAX whose fp32 group sums overflow, and a
+    single outlier; every entry within 1e-6 of the oracle (float64)."""
+    print(f"case: grad_stats tiny/constant/offset {dtype}", flush=True)
+    n = 3 * 32768 + 5
+    g = torch.Generator().manual_seed(11)
+    r = torch.randn(n, generator=g)
+    cases = {
+        "tiny": r * 1e-25,
+        "tiny offset": 2.0 ** -70 + r * 2.0 ** -80,
+        "constant": torch.full((n,), 0.37),
+        "zeros": torch.zeros(n),
+        "zeros and one": torch.zeros(n).index_fill_(0, torch.tensor([40000]), 1.0),
+        "offset": 1000.0 + r * 1e-3,
+        "outlier": (r * 1e-3).index_fill_(0, torch.tensor([7]), 50.0),
+        "mixed tiny": torch.where(torch.arange(n) < 40000, r * 1e-30, r * 1e-3),
+    }
+    if dtype == torch.float32:
+        cases["near FLT_MAX"] = torch.where(torch.arange(n) % 8 < 2, 1.5e38, 1e-3 * r)
+        cases["near FLT_MAX, opposite signs"] = torch.where(torch.arange(n) % 8 == 0, 2e38,
+                                                            torch.where(torch.arange(n) % 8 == 1, -2e38, r))
+    vs = [v.to(dtype).to(DEV) for v in cases.values()]
+    got = mdq_hip.grad_stats(vs).cpu().numpy()
+    for (name, _), v, row in zip(cases.items(), vs, got):
+        ref = orc.grad_stats(v.float().cpu().numpy())
+        assert np.array_equal(np.isnan(row), np.isnan(ref)) and np.array_equal(np.isinf(row), np.isinf(ref)), \
+            (name, row, ref)
+        fin = np.isfinite(ref)
+        np.testing.assert_allclose(row[fin], ref[fin], rtol=1e-6, atol=0, err_msg=name)
+
+
 @pytest.mark.parametrize("c_exp", [10, 20, 30])
 def test_variance_exact_for_large_means(c_exp):
     """x = c + d (i mod 16), d the fp32 spacing at c, over 100,003 elements (four tiles, a
