@@ -108,12 +108,25 @@ def zero_codes(like: torch.Tensor, kind: int) -> Tuple[torch.Tensor, torch.Tenso
     return m.zero_(), v.zero_()
 
 
-def decode(exp_avg: torch.Tensor, exp_avg_sq: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
-    """The integer code values ``(m, v)`` as int64 tensors of ``exp_avg``'s shape."""
+# The narrowest signed integer type holding every code value of a layout (uint16 v needs
+# int32, uint32 v int64).
+_VALUE_DTYPE = {STORE_P4: torch.int16, STORE_S8: torch.int16, STORE_S16: torch.int32, STORE_S32: torch.int64}
+_WIDTH = {torch.int16: 0, torch.int32: 1, torch.int64: 2}
+
+
+def value_dtype(*kinds: int) -> torch.dtype:
+    """The narrowest signed integer type holding the code values of all ``kinds``."""
+    return max((_VALUE_DTYPE[k] for k in kinds), key=_WIDTH.__getitem__)
+
+
+def decode(exp_avg: torch.Tensor, exp_avg_sq: torch.Tensor,
+           dtype: torch.dtype = torch.int64) -> Tuple[torch.Tensor, torch.Tensor]:
+    """The integer code values ``(m, v)`` as ``dtype`` tensors of ``exp_avg``'s shape
+    (``dtype`` must hold the layout's values: ``value_dtype(layout)`` or wider)."""
     if layout_of(exp_avg, exp_avg_sq) == STORE_P4:
-        byte = exp_avg.to(torch.int64)
+        byte = exp_avg.to(dtype)
         return (byte & 15) - 8, byte >> 4
-    return exp_avg.to(torch.int64), exp_avg_sq.to(torch.int64)
+    return exp_avg.to(dtype), exp_avg_sq.to(dtype)
 
 
 def encode(m: torch.Tensor, v: torch.Tensor, kind: int) -> Tuple[torch.Tensor, torch.Tensor]:
@@ -131,5 +144,7 @@ def restore(exp_avg: torch.Tensor, exp_avg_sq: torch.Tensor, kind: int) -> Tuple
     tensors have no values, so only their dtypes change."""
     if exp_avg.numel() == 0:
         return empty_codes(exp_avg, kind)
-    m, v = decode(exp_avg, exp_avg_sq)
+    # values in the narrowest type that holds both layouts' ranges: the passes move
+    # 2 or 4 bytes per value rather than 8, as the reference's casts do
+    m, v = decode(exp_avg, exp_avg_sq, value_dtype(layout_of(exp_avg, exp_avg_sq), kind))
     return encode(m, v, kind)
