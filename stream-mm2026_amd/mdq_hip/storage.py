@@ -144,7 +144,12 @@ def restore(exp_avg: torch.Tensor, exp_avg_sq: torch.Tensor, kind: int) -> Tuple
     tensors have no values, so only their dtypes change."""
     if exp_avg.numel() == 0:
         return empty_codes(exp_avg, kind)
+    src, dst = LAYOUTS[layout_of(exp_avg, exp_avg_sq)], LAYOUTS[kind]
+    if not src.packed and not dst.packed and dst.m_lo <= src.m_lo and src.m_hi <= dst.m_hi \
+            and src.v_hi <= dst.v_hi:
+        # every value fits the destination: the map is a plain cast
+        return exp_avg.to(dst.m_dtype, copy=True), exp_avg_sq.to(dst.v_dtype, copy=True)
     # values in the narrowest type that holds both layouts' ranges: the passes move
-    # 2 or 4 bytes per value rather than 8, as the reference's casts do
-    m, v = decode(exp_avg, exp_avg_sq, value_dtype(layout_of(exp_avg, exp_avg_sq), kind))
+    # 2 or 4 bytes per value rather than 8
+    m, v = decode(exp_avg, exp_avg_sq, value_dtype(src.kind, kind))
     return encode(m, v, kind)

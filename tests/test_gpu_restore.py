@@ -134,29 +134,34 @@ def test_restore_matches_separate_passes(src, dst, B):
 @pytest.mark.parametrize("cls", [MDQAdamWSimple, MDQAdamWSimpleFusedIO])
 @pytest.mark.parametrize("B", [64, 256, 512])
 def test_optimizer_fused_transitions_match_separate_passes(cls, B):
-    """Bit-width changes 16 -> 4 -> 8 -> 16 -> 4 -> 32 -> 8 -> 4 with the fused transitions on and
-    off, identical params and grads; B = 512 has no restore kernels (separate passes in both)."""
+    """Bit-width changes 16 -> 4 -> 8 -> 16 -> 4 -> 32 -> 8 -> 4 with the fused transitions on,
+    off, and with the codes moved by torch passes on the device (``_device_transitions = False``),
+    identical params and grads; B = 512 has no restore kernels (separate passes)."""
     print(f"case: {cls.__name__} fused transitions B={B}", flush=True)
     shapes = [(700, 13), (4096,), (129,), (3, 1000)]
     cpu, gpu = build(shapes, seed=21)
     gpu2 = [torch.nn.Parameter(p.detach().clone()) for p in gpu]
-    on, off = cls(gpu, bits=4, block_size=B), cls(gpu2, bits=4, block_size=B)
+    gpu3 = [torch.nn.Parameter(p.detach().clone()) for p in gpu]
+    on, off, tor = (cls(g, bits=4, block_size=B) for g in (gpu, gpu2, gpu3))
     off._fused_transitions = False
+    tor._device_transitions = False
     for t, bits in enumerate([4, 8, 16, 4, 32, 8, 4, 4], start=1):
-        for o in (on, off):
+        for o in (on, off, tor):
             o.param_groups[0]["bits"] = bits
         grads(cpu, gpu, 300 + t)
-        for a, b in zip(gpu, gpu2):
+        for a, b, c in zip(gpu, gpu2, gpu3):
             b.grad = a.grad.clone()
-        on.step()
-        off.step()
+            c.grad = a.grad.clone()
+        for o in (on, off, tor):
+            o.step()
         torch.cuda.synchronize()
-        for i, (a, b) in enumerate(zip(gpu, gpu2)):
-            sa, sb = on.state[a], off.state[b]
-            assert sa["step"] == sb["step"] and sa["current_bit"] == sb["current_bit"] == bits
-            for k in ("exp_avg", "exp_avg_sq", "scale_m", "scale_v", "v_min"):
-                assert sa[k].dtype == sb[k].dtype and torch.equal(sa[k], sb[k]), (t, bits, i, k)
-            assert torch.equal(a.detach(), b.detach()), (t, bits, i)
+        for other, params in ((off, gpu2), (tor, gpu3)):
+            for i, (a, b) in enumerate(zip(gpu, params)):
+                sa, sb = on.state[a], other.state[b]
+                assert sa["step"] == sb["step"] and sa["current_bit"] == sb["current_bit"] == bits
+                for k in ("exp_avg", "exp_avg_sq", "scale_m", "scale_v", "v_min"):
+                    assert sa[k].dtype == sb[k].dtype and torch.equal(sa[k], sb[k]), (t, bits, i, k)
+                assert torch.equal(a.detach(), b.detach()), (t, bits, i)
 
 
 @pytest.mark.parametrize("src,dst", [(2, 0), (0, 1), (1, 2), (3, 0)],
