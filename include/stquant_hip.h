@@ -48,7 +48,7 @@ enum stq_dtype {
 
 enum stq_rounding {
     STQ_ROUND_NEAREST = 0,    /* round half away from zero (the reference) */
-    STQ_ROUND_STOCHASTIC = 1  /* floor(x + u), u from Philox4x32-10 (codes <= 16 bits) */
+    STQ_ROUND_STOCHASTIC = 1  /* floor(x + u), u from Philox4x32-7 (codes <= 16 bits) */
 };
 
 /*
@@ -289,6 +289,8 @@ void stq_host_round_half_away(const float *u, const float *d, float *out, int64_
 /* out[i] = x[i] / (2^bits - 1) as the kernel computes the new v scale
  * (a correction step that must equal IEEE division). */
 void stq_host_div_code_range(const float *x, float *out, int64_t n, int bits);
+/* The library's Philox4x32 round function run 10 times (Random123's default, whose
+ * known-answer vectors pin it); the stochastic step runs the same rounds 7 times. */
 void stq_host_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]);
 
 #ifdef __cplusplus
