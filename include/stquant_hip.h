@@ -151,11 +151,12 @@ int stq_multi_tensor_mdq_adamw(const stq_tensor *tensors, int n_tensors,
  * The descriptor table lives in a fixed device array of the library
  * (STQ_NOALLOC_MAX_TENSORS * 184 bytes = 736 KiB, held by every GPU the
  * library runs on until the process ends) and is copied there from a static
- * host buffer.  That copy is synchronous: the call returns after the work
- * queued on `stream` before it has finished.  All calls on one GPU share the
- * array: calls on the same stream are ordered, but calls on different streams
- * of one GPU race (a later call can overwrite the table an earlier call's
- * kernel is still reading) and must be ordered by the caller.
+ * host buffer with hipMemcpyAsync on `stream`: the host buffer is free again
+ * when that call returns (pageable memory), and on the device the copy runs in
+ * stream order, after the work queued before it.  All calls on one GPU share
+ * the array: calls on the same stream are ordered, but calls on different
+ * streams of one GPU race (a later call can overwrite the table an earlier
+ * call's kernel is still reading) and must be ordered by the caller.
  */
 int stq_multi_tensor_mdq_adamw_noalloc(const stq_tensor *tensors, int n_tensors,
                                        int grad_dtype, int exp_avg_dtype, int exp_avg_sq_dtype,

@@ -690,9 +690,9 @@ int run_noalloc(const stq_tensor *tensors, int n_tensors, int grad_dt, int ea_dt
     }
     long long *tb = reinterpret_cast<long long *>(g_noalloc_stage + (size_t)nd * sizeof(MdqDesc));
     for (int i = 0; i < nd; ++i) tb[i] = descs[i].tile_begin;
-    // The staging buffer is pageable memory, so the copy is synchronous: it runs after
-    // the work queued on `stream` before it (an earlier call's kernel has finished
-    // reading the table), and the buffer is free again when it returns.
+    // The staging buffer is pageable memory: hipMemcpyAsync has read it when it returns
+    // (so the next call may refill it), and on the device the copy runs in stream order,
+    // after an earlier call's kernel on this stream has finished reading the table.
     e = hipMemcpyAsync(g_scratch_dev[dev], g_noalloc_stage, (size_t)nd * (sizeof(MdqDesc) + sizeof(long long)),
                        hipMemcpyHostToDevice, stream);
     if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(descriptors -> scratch)");

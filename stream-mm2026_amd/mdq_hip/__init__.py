@@ -214,8 +214,7 @@ class MultiTensorPlan:
     def run(self, profile_cycles: Optional[torch.Tensor] = None, *, noalloc: bool = False) -> None:
         """One launch over the plan's tensors on the current stream.  ``noalloc`` takes the
         library's allocation-free entry point (``stq_multi_tensor_mdq_adamw_noalloc``: at
-        most NOALLOC_MAX_TENSORS tensors, the call returns once the stream's earlier work has
-        finished)."""
+        most NOALLOC_MAX_TENSORS tensors, one table per GPU shared by all its streams)."""
         if self.n == 0:
             return
         if self.device.type != "cuda":
