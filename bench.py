@@ -501,6 +501,20 @@ def counter_means(pmc_dir, kernel, last=None):
     return out
 
 
+def copy_calibration(dev, gib: float) -> None:
+    """Three plain copies of ``gib`` GiB: a known byte count for scaling FETCH_SIZE / WRITE_SIZE."""
+    import torch
+
+    n = int(gib * (1 << 30)) // 4
+    src = torch.ones(n, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"copy calibration: 3 x {n * 4} bytes read + written")
+    del src, dst
+
+
 def profile_summary(args):
     """Writes ``<out>.json`` and ``<out>.md`` from rocprofv3 runs of this script: a kernel trace
     (``--trace``), and optionally FETCH_SIZE / WRITE_SIZE runs (``--fetch`` / ``--write``) made
@@ -508,10 +522,15 @@ def profile_summary(args):
     shapes_fn, gdt, cfg_bits, B = CONFIGS[args.config]
     bits = cfg_bits if args.bits is None else args.bits
     N = sum(n for _, n in shapes_fn())
-    alg = bytes_per_param(2 if gdt == "bf16" else 4, bits, B) * N
+    if args.grad_stats:
+        # the statistics kernel reads every grad once
+        alg = (2 if gdt == "bf16" else 4) * N
+        workload = f"grad statistics of the {args.config} set, {gdt} grads"
+    else:
+        alg = bytes_per_param(2 if gdt == "bf16" else 4, bits, B) * N
+        workload = f"{args.config}, {bits}-bit codes, B={B}, {gdt} grads, {args.rounding} rounding"
     t = trace_stats(args.trace, args.kernel, args.skip)
-    out = dict(kernel=t["name"], workload=f"{args.config}, {bits}-bit codes, B={B}, {gdt} grads, "
-                                            f"{args.rounding} rounding", params=N,
+    out = dict(kernel=t["name"], workload=workload, params=N,
                dispatches=t["dispatches"], warmup_dispatches_dropped=t["skipped"], calls=t["timed"],
                avg_ns=t["avg_ns"], min_ns=t["min_ns"], max_ns=t["max_ns"], avg_ns_with_warmup=t["all_avg_ns"],
                algorithmic_bytes=alg, achieved_gbs=alg / t["avg_ns"], frac_of_peak=alg / t["avg_ns"] / HBM_PEAK_GBS)
@@ -599,6 +618,9 @@ def main():
     ap.add_argument("--sq", help="with --profile-summary: rocprofv3 --pmc SQ_* output directory")
     ap.add_argument("--kernel", default="mdq_step_kernel", help="with --profile-summary: kernel name substring")
     ap.add_argument("--skip", type=int, default=0, help="with --profile-summary: warm-up dispatches to drop")
+    ap.add_argument("--grad-stats", action="store_true",
+                    help="with --profile-summary: the kernel is the grad-statistics kernel (algorithmic bytes = "
+                         "the config's grads, read once)")
     ap.add_argument("--cmd", action="append", default=[], help="with --profile-summary: a command to record")
     args = ap.parse_args()
     if args.profile_summary:
@@ -625,8 +647,11 @@ def main():
                           "data": "synthetic", "configs": transitions(max(1, args.steps // 10))}), flush=True)
         return
     if args.bit_decision:
+        res = bit_decision(args.steps)
+        if args.copy_gib > 0:
+            copy_calibration(dev, args.copy_gib)
         print(json.dumps({"metric": "MDQ bit decision per update step (ms)", "n_gpus": 1, "steps": args.steps,
-                          "data": "synthetic", "configs": bit_decision(args.steps)}), flush=True)
+                          "data": "synthetic", "configs": res}), flush=True)
         return
     if args.e2e_gpt2:
         print(json.dumps(e2e_gpt2(args.e2e_steps, args.warmup, args.e2e_out)), flush=True)
@@ -674,14 +699,7 @@ def main():
     log(f"timed {args.steps} steps: {kernel_ms:.3f} ms/step (events), wall {wall / args.steps * 1e3:.3f} ms/step")
 
     if args.copy_gib > 0:
-        n = int(args.copy_gib * (1 << 30)) // 4
-        src = torch.ones(n, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        log(f"copy calibration: 3 x {n * 4} bytes read + written")
-        del src, dst
+        copy_calibration(dev, args.copy_gib)
 
     N = w["N"]
     bpp = bytes_per_param(w["grad_bytes"], w["bits"], w["B"])
