@@ -1,6 +1,7 @@
 """bench.py's host-side contract, on the CPU: the one-GPU exit, the metric names of the configs,
-the algorithmic byte counts the roofline figure divides by, and the fields of the CPU-baseline
-record (a short sample of the oracle)."""
+the algorithmic byte counts the roofline figure divides by, the fields of the CPU-baseline
+record (a short sample of the oracle), and the rocprofv3 summaries behind the committed
+profiles (warm-up dispatches dropped, counters scaled by the calibration copies)."""
 import os
 import subprocess
 import sys
@@ -50,3 +51,57 @@ def test_cpu_baseline_record():
     assert c["value"] > 0 and c["value_1thread"] > 0
     assert abs(c["gbs"] - c["value"] * 12.1875 / 1e9) < 1e-9 * c["gbs"] + 1e-12
     assert c["cpu_model"] and "oracle/mdq_oracle.c" in c["sample"]
+
+
+def _write_csv(path, header, rows):
+    import csv
+    os.makedirs(os.path.dirname(path), exist_ok=True)
+    with open(path, "w", newline="") as f:
+        w = csv.writer(f)
+        w.writerow(header)
+        w.writerows(rows)
+
+
+def test_profile_summary_drops_warmup_and_calibrates_on_the_last_copies(tmp_path):
+    """``--profile-summary`` on synthetic rocprofv3 CSVs: the kernel time averages only the
+    dispatches after the warm-up ones (dispatch order, not file order), and FETCH_SIZE /
+    WRITE_SIZE are scaled by what the last three copies of known size read, not by an earlier
+    set-up copy of another size."""
+    k = "void mdq::mdq_step_kernel<0, 0, 1, 7, false>(...)"
+    cp = "__amd_rocclr_copyBuffer"
+    # 2 warm-up dispatches of 20 ms, then 4 of 10 ms, listed out of order
+    trace = [(k, 6, 0, 10_000_000), (k, 1, 0, 20_000_000), (k, 4, 0, 10_000_000), (k, 2, 0, 20_000_000),
+             (k, 3, 0, 10_000_000), (k, 5, 0, 10_000_000), (cp, 7, 0, 1)]
+    _write_csv(str(tmp_path / "tr" / "x" / "t_kernel_trace.csv"),
+               ["Kernel_Name", "Dispatch_Id", "Start_Timestamp", "End_Timestamp"], trace)
+    gib = 4
+    copy_kib = gib * (1 << 30) / 1024
+    fetch = [(k, 1, "FETCH_SIZE", 1000.0), (k, 2, "FETCH_SIZE", 3000.0),
+             (cp, 3, "FETCH_SIZE", 123.0),                                    # set-up copy, another size
+             (cp, 4, "FETCH_SIZE", copy_kib / 2), (cp, 5, "FETCH_SIZE", copy_kib / 2),
+             (cp, 6, "FETCH_SIZE", copy_kib / 2)]
+    write = [(k, 1, "WRITE_SIZE", 500.0), (k, 2, "WRITE_SIZE", 1500.0),
+             (cp, 3, "WRITE_SIZE", 7.0),
+             (cp, 4, "WRITE_SIZE", copy_kib), (cp, 5, "WRITE_SIZE", copy_kib), (cp, 6, "WRITE_SIZE", copy_kib)]
+    hdr = ["Kernel_Name", "Dispatch_Id", "Counter_Name", "Counter_Value"]
+    _write_csv(str(tmp_path / "f" / "f_counter_collection.csv"), hdr, fetch)
+    _write_csv(str(tmp_path / "w" / "w_counter_collection.csv"), hdr, write)
+    out = str(tmp_path / "summary")
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--profile-summary", out,
+                        "--config", "gpt2", "--trace", str(tmp_path / "tr"), "--fetch", str(tmp_path / "f"),
+                        "--write", str(tmp_path / "w"), "--skip", "2", "--copy-gib", str(gib),
+                        "--kernel", "mdq_step_kernel"], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    import json
+    with open(out + ".json") as f:
+        d = json.load(f)
+    assert d["dispatches"] == 6 and d["calls"] == 4 and d["avg_ns"] == 10_000_000
+    assert d["avg_ns_with_warmup"] == (2 * 20_000_000 + 4 * 10_000_000) / 6
+    assert d["fetch_scale"] == 2.0 and d["write_scale"] == 1.0
+    # kernel: mean FETCH 2000 KiB x 2 + mean WRITE 1000 KiB x 1
+    assert d["traffic_bytes"] == (2000.0 * 2 + 1000.0) * 1024
+    alg = bench.bytes_per_param(4, 4, 128) * 124_439_808
+    assert d["algorithmic_bytes"] == alg and abs(d["frac_of_peak"] - alg / 1e7 / 8000.0) < 1e-12
+    with open(out + ".md") as f:
+        md = f.read()
+    assert "average over the 4 timed launches **10.000 ms**" in md
