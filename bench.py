@@ -252,10 +252,11 @@ def sweep_config5(dev, steps: int, warmup: int, packed_views: bool = False, view
                 view_align=view_align if packed_views else ALIGN_ELEMS, points=points)
 
 
-def e2e_gpt2(steps: int, warmup: int, out_path):
+def e2e_gpt2(steps: int, warmup: int, out_path, vocab_used=None):
     """GPT-2 small, seq 1024, micro-batch 8, bf16 autocast, 4-bit fused AdamW
     with stochastic rounding vs the same optimizer in nearest mode (the reference's arithmetic) and
-    torch AdamW, each on identical seeded synthetic tokens."""
+    torch AdamW, each on identical seeded synthetic tokens: uniform over the vocabulary, or over its
+    first ``vocab_used`` ids (a unigram task the model learns)."""
     import gpt2_pretrain
 
     runs = {}
@@ -265,15 +266,17 @@ def e2e_gpt2(steps: int, warmup: int, out_path):
                                       # the reference's default: score-based bit widths (MDQ schedule)
                                       ("mdq_schedule_nearest", "MDQAdamW-Simple-FusedIO", "nearest", None)):
         log(f"gpt2 e2e: {key} ({steps} steps)")
+        kw = {} if vocab_used is None else {"vocab_used": vocab_used}
         runs[key] = gpt2_pretrain.train(name, steps=steps, warmup=warmup, rounding=rounding or "nearest",
-                                        bits=bits, log_every=50)
+                                        bits=bits, log_every=50, **kw)
     la = runs["mdq4_stochastic"]["History"]["loss"]
     lb = runs["mdq4_nearest"]["History"]["loss"]
     lc = runs["adamw32"]["History"]["loss"]
     res = {
         "metric": "GPT-2 small e2e: optimizer share of step time and loss-curve gap", "n_gpus": 1,
         "steps": steps, "warmup": warmup, "dtype": "bf16 autocast, fp32 optimizer math",
-        "data": "synthetic uniform tokens (seeded, identical across runs)",
+        "data": ("synthetic uniform tokens (seeded, identical across runs)" if vocab_used is None else
+                 f"synthetic tokens uniform over the first {vocab_used} ids (seeded, identical across runs)"),
         "config": {"workload": "gpt2-small e2e", "global_batch": 8, "seq_len": 1024, "bits": 4, "block": 128},
         "loss_gap_stochastic_vs_nearest": {
             "max_rel_smoothed10": gpt2_pretrain.compare_loss_curves(la, lb, 10),
@@ -599,6 +602,8 @@ def main():
     ap.add_argument("--e2e-gpt2", action="store_true",
                     help="BASELINE config 3: GPT-2 small pretraining, stochastic vs nearest vs AdamW")
     ap.add_argument("--e2e-steps", type=int, default=300)
+    ap.add_argument("--e2e-vocab", type=int, default=None,
+                    help="with --e2e-gpt2: tokens from the first N ids only (a learnable task)")
     ap.add_argument("--e2e-out", default=None, help="also write the loss histories as JSON here")
     ap.add_argument("--transitions", action="store_true",
                     help="time storage-changing optimizer steps, device conversions vs torch passes")
@@ -654,7 +659,7 @@ def main():
                           "data": "synthetic", "configs": res}), flush=True)
         return
     if args.e2e_gpt2:
-        print(json.dumps(e2e_gpt2(args.e2e_steps, args.warmup, args.e2e_out)), flush=True)
+        print(json.dumps(e2e_gpt2(args.e2e_steps, args.warmup, args.e2e_out, args.e2e_vocab)), flush=True)
         return
     w = build_workload(args.config, dev, bits=args.bits)
     plan = w["plan"]
