@@ -804,9 +804,9 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
                 inv_dv = 1.0f / dv;
             }
             float um[EPL], uv[EPL];
-            // Philox4x32-10 per 4-element quad of the tensor: counter
-            // (quad index lo, hi, tensor id, step), key = seed; word i of the
-            // output serves element 4q+i (low half -> m, high half -> v).
+            // Philox4x32 (MDQ_SR_ROUNDS rounds) per 4-element quad of the tensor:
+            // counter (quad index lo, hi, tensor id, step), key = seed; word i of
+            // the output serves element 4q+i (low half -> m, high half -> v).
             // Element indices count from rng_origin (a multiple of B, so of 4
             // wherever a lane owns whole quads).
             if constexpr (C::QPL > 0) {
