@@ -9,9 +9,9 @@
 //      sum g^2 (fp32 squares, as the reference's grad * grad) and sum |g|.
 //      Each thread loads its 64 elements with 16-byte loads and sums x, x^2 and |x|
 //      over each load pairwise in fp32 (at most 3 roundings, 1.8e-7 of the summed
-//      magnitudes), and these short sums across loads in fp64.  The kernel is
-//      VALU-bound near the HBM roofline, so the common path costs about six
-//      instructions per element.  The thread's M2 comes from sum x^2 - (sum x)^2 / 64
+//      magnitudes), and these short sums across loads in fp64.  Near the HBM
+//      roofline the kernel is close to VALU-bound (about ten lane instructions per
+//      element fit in the memory time); this path takes about seven.  The thread's M2 comes from sum x^2 - (sum x)^2 / 64
 //      where that cancellation loses at most a bit; where the mean dominates the
 //      spread the registers are summed again as deviations from the thread's fp32
 //      mean, and non-finite or tiny (squares below fp32's normal range) values are
