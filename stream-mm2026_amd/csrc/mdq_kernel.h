@@ -854,9 +854,12 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
                     any = any || redo[e];
                 }
                 if (__builtin_amdgcn_ballot_w64(any)) {
+                    const bool flat = kx == kn;          // code floor(0 + uv) = 0
 #pragma unroll
-                    for (int e = 0; e < EPL; ++e)
-                        if (redo[e]) qvf[e] = floor_(fma_(mdq_logf(v[e] + 1e-12f) - s_vmin, inv_dv, uv[e]));
+                    for (int e = 0; e < EPL; ++e) {
+                        if (flat) qvf[e] = 0.0f;
+                        else if (redo[e]) qvf[e] = floor_(fma_(mdq_logf(v[e] + 1e-12f) - s_vmin, inv_dv, uv[e]));
+                    }
                 }
             } else {
                 // non-finite quotients give code 0, as in the nearest path below
@@ -921,11 +924,15 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
                     any = any || redo[e] || redo_m[e];
                 }
                 if (__builtin_amdgcn_ballot_w64(any)) {
+                    // every x of a flat block equals xmin, so log x - vmin = 0 and the
+                    // code is 0 (its tiny dv flags every element above)
+                    const bool flat = kx == kn;
 #pragma unroll
                     for (int e = 0; e < EPL; ++e) {
                         if (redo_m[e])
                             qmf[e] = __builtin_copysignf(mdq_round_half_away(fabsf(m[e]) * msc, dmq, ilm, hdm), m[e]);
-                        if (redo[e]) qvf[e] = mdq_round_half_away(mdq_logf(v[e] + 1e-12f) - s_vmin, dv, ilv, hdv);
+                        if (flat) qvf[e] = 0.0f;
+                        else if (redo[e]) qvf[e] = mdq_round_half_away(mdq_logf(v[e] + 1e-12f) - s_vmin, dv, ilv, hdv);
                     }
                 }
             } else {

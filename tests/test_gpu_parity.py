@@ -267,6 +267,37 @@ def test_stochastic_rounding_bit_exact(storage, bits):
         c.check(p_prev)
 
 
+@pytest.mark.parametrize("storage,bits", [(orc.STORE_P4, 4), (orc.STORE_S8, 8)], ids=["p4", "s8"])
+@pytest.mark.parametrize("rounding", ["nearest", "stochastic"])
+def test_flat_blocks_beside_ordinary_ones(storage, bits, rounding):
+    """Blocks whose v + 1e-12 is the same float in every element (zero grads every step, or one
+    grad value for the whole block) next to ordinary blocks in the same waves, 8 steps from a fresh
+    state.  Their v codes are 0 (log x - vmin = 0 exactly), which the fast path sets without the
+    per-element logs; codes, scales and params against the oracle after every step."""
+    print(f"case: flat blocks storage={storage} bits={bits} {rounding}", flush=True)
+    rng = np.random.default_rng(31 + bits)
+    B = 128
+    n = B * 4 * 256
+    nb = n // B
+    c = Case(n, B, storage, rng)
+    kind = rng.integers(0, 4, nb)            # 0: zero grads, 1: one value per block, 2-3: ordinary
+    assert (kind == 0).any() and (kind == 1).any()
+    rmode = orc.ROUND_STOCHASTIC if rounding == "stochastic" else orc.ROUND_NEAREST
+    for step in range(1, 9):
+        g = (rng.standard_normal(n) * 1e-3).astype(np.float32)
+        gb = g.reshape(nb, B)
+        gb[kind == 0] = 0.0
+        gb[kind == 1] = np.float32(1e-3 * (1 + step % 3))
+        p_prev = c.p.copy()
+        c.oracle_step(g, step, bits, rounding=rmode, seed=77, tensor_id=5)
+        mdq_hip.multi_tensor_step([c.entry(to_dev(g), step, bits, tensor_id=5)], B, rounding=rounding, seed=77)
+        c.check(p_prev)
+    # the flat blocks did end at code 0 with v_min at their common log
+    cm, cv = c.state[0], c.state[1]
+    vcodes = (cm >> 4) if cv is None else cv
+    assert np.all(vcodes.reshape(nb, B)[kind == 0] == 0)
+
+
 def test_multi_tensor_ragged_heavy_tail():
     """Config-5-style: many tensors with log-uniform sizes (mostly not multiples of B),
     Student-t grads with all-zero blocks and x1000 outliers, per-tensor steps and
