@@ -52,7 +52,9 @@ from typing import Optional
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIB_PATH = os.path.join(_HERE, "libmdq_oracle.so")
+# MDQ_ORACLE_LIB points the tests at another build of mdq_oracle.c (the mutation tests load
+# builds with one planted mistake each, to show that the pinning tests catch it).
+_LIB_PATH = os.environ.get("MDQ_ORACLE_LIB") or os.path.join(_HERE, "libmdq_oracle.so")
 
 STORE_P4, STORE_S8, STORE_S16, STORE_S32 = 0, 1, 2, 3
 GRAD_F32, GRAD_BF16, GRAD_F16 = 0, 1, 2

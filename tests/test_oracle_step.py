@@ -239,6 +239,28 @@ def test_stochastic_rounding_unbiased_and_two_valued():
     assert np.mean(z) < 1.0 and np.max(z) < 6.0
 
 
+def test_stochastic_stream_depends_on_step_tensor_and_seed():
+    """The random numbers are a function of (element, tensor id, step, seed): the same state and
+    grads stepped with another step number, tensor id or seed round differently somewhere, and
+    about half of the elements (each code is an independent coin flip where the quotient sits
+    between two codes) change; the same four values reproduce the codes exactly."""
+    rng = np.random.default_rng(12)
+    n, B = 128 * 16, 128
+    g = (rng.standard_normal(n) * 1e-3).astype(np.float32)
+
+    def codes(step, tensor_id, seed):
+        st = fresh(n, B, orc.STORE_S8)
+        run(np.zeros(n, np.float32), g, st, step=step, bits=4, B=B, storage=orc.STORE_S8,
+            rounding=orc.ROUND_STOCHASTIC, seed=seed, tensor_id=tensor_id)
+        return np.concatenate([st[0].astype(np.int64), st[1].astype(np.int64)])
+
+    base = codes(3, 5, 99)
+    assert np.array_equal(base, codes(3, 5, 99))
+    for other in (codes(4, 5, 99), codes(3, 6, 99), codes(3, 5, 100)):
+        frac = np.mean(base != other)
+        assert 0.2 < frac < 0.8, frac
+
+
 @pytest.mark.parametrize("bad", [dict(block_size=96), dict(bits=5, storage=orc.STORE_P4),
                                  dict(bits=9, storage=orc.STORE_S8), dict(step=0)])
 def test_rejects_invalid(bad):
