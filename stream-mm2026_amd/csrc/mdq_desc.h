@@ -3,7 +3,7 @@
 // The host launcher (mdq_capi.cpp) packs one MdqDesc per tensor into a single
 // device buffer; the kernel walks the whole param/grad/state list from it.
 // Each tensor owns the contiguous global tile range [tile_begin, tile_end);
-// a tile is 256 lanes x elements-per-lane and never straddles two tensors.
+// a tile is one workgroup (tile_elems below) and never straddles two tensors.
 #pragma once
 #include <stdint.h>
 

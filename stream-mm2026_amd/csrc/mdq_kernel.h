@@ -21,6 +21,8 @@
 //   exchange between the two waves of a 1024-element block.  They skip NaN as
 //   the reference's fmaxf / fminf trees do, and non-finite quotients give
 //   code 0, as its (int) conversion of NaN does.
+// * A tile whose params do not start on a 128-byte line (views of one buffer)
+//   writes them line by line through LDS (store_p_lines).
 // * Packed 4-bit v codes dequantise through a 16-entry exp table per block
 //   built in LDS (16 exp per block instead of one per element).
 // * Requant uses mdq_round_half_away (exact fp32) for code widths <= 16 bits
@@ -509,14 +511,57 @@ __device__ __forceinline__ float dequant_m(float code, float sm, float neg8sm)
 // all pointers are 16-byte aligned, so vector accesses are used.  TILE_UNALIGNED_PG:
 // the tile lies inside the tensor and the codes are aligned, but p or the grads
 // are not (views at arbitrary element offsets of one buffer, as ZeRO-style flat
-// partitions hand them over): codes move as in TILE_VECTOR, and p and grads move
-// as the same 4-element vectors at element-aligned addresses.
+// partitions hand them over): codes move as in TILE_VECTOR, and p and grads are
+// loaded as the same 4-element vectors at element-aligned addresses.  In both
+// modes a p that does not start on a 128-byte line is stored through LDS
+// (store_p_lines).
 // TILE_GUARDED: every access element by element, guarded by idx < numel.
 enum TileMode : int { TILE_GUARDED = 0, TILE_VECTOR = 1, TILE_UNALIGNED_PG = 2 };
 
+// A whole tile's p stores when p does not start on a 128-byte line (pst: TILE floats
+// of LDS, 16-byte aligned, holding the tile's new p; dl = the tile's offset in its
+// first line, in elements, 1..31).  The lanes' own 16-byte pieces would split every
+// line between two store instructions wherever a block's span of lanes does not
+// start on a line (every line at B = 64), and partial line writes cost memory time
+// far beyond their bytes.  Here the full lines go out as aligned 16-byte vectors
+// from one instruction per line, and the two edge lines, which the neighbouring
+// tiles (or views) share, element by element through L2 (temporal stores: the two
+// halves of such a line then mostly meet in L2 and leave as one line).
+template <int THREADS, int TILE>
+__device__ __forceinline__ void store_p_lines(float *p, const float *pst, uint32_t dl)
+{
+    static_assert(TILE % 32 == 0 && TILE >= 64 && THREADS >= 32, "tile geometry of the staged store");
+    if constexpr (THREADS == 64) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    } else {
+        __syncthreads();
+    }
+    // position q of the tile's lines holds element q - dl: line 0 starts dl
+    // elements before the tile, line TILE / 32 ends 32 - dl elements after it
+    const uint32_t t = threadIdx.x;
+    float *pl = p - dl;
+    if (t < 32u) {
+        // edge elements: positions dl .. 31 (line 0) and TILE .. TILE + dl - 1 (last line)
+        const uint32_t q = t < dl ? TILE + t : t;
+        st_g<float>(pst[q - dl], pl + q);
+    }
+    constexpr int NV = TILE / 4 - 8;                      // 16-byte vectors of lines 1 .. TILE/32 - 1
+#pragma unroll
+    for (int r = 0; r < (NV + THREADS - 1) / THREADS; ++r) {
+        const uint32_t w = t + r * THREADS;
+        if (w < (uint32_t)NV) {
+            const uint32_t q = 32 + 4 * w, e = q - dl;
+            const vf4 o = {pst[e], pst[e + 1], pst[e + 2], pst[e + 3]};
+            st_nt<vf4>(o, pl + q);
+        }
+    }
+}
+
 template <int SRC, int DST, int GT, int LOG2B, bool SR, int MODE>
 __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int lane, int wave,
-                                              float *lut, int32_t *xw, unsigned long long seed,
+                                              float *lut, int32_t *xw, float *pst, unsigned long long seed,
                                               bool prof_on, ProfAcc &pa)
 {
     using C = Cfg<LOG2B>;
@@ -1001,6 +1046,9 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
     if constexpr (FULL && C::QPL > 0) {
         const MdqDesc dt = tile_view<SRC, DST, GT>(d, tbase);
         const MdqDesc ot = out_view<SRC, DST>(dt);
+        // p's offset in its 128-byte line, in elements (the same for every tile of the
+        // tensor); nonzero: the lanes' p go to LDS and store_p_lines writes them
+        const uint32_t dl = (uint32_t)(reinterpret_cast<uintptr_t>(dt.p) >> 2) & 31u;
 #pragma unroll
         for (int k = 0; k < C::QPL; ++k) {
             const uint32_t i = lbase + 4 * lane_quad<PAIRED, LOG2B>(j, k);
@@ -1009,13 +1057,15 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
                 else CodeIO<DST>::store4(ot, i, qmi + 4 * k, qvi + 4 * k);
             }
             const vf4 o = {pv[4 * k + 0], pv[4 * k + 1], pv[4 * k + 2], pv[4 * k + 3]};
-            if constexpr (VEC_PG) st_nt<vf4>(o, dt.p + i);
+            if (dl != 0u) *(vf4 *)(pst + i) = o;
+            else if constexpr (VEC_PG) st_nt<vf4>(o, dt.p + i);
             else st_nt_al<vf4, 4>(o, dt.p + i);
         }
         if constexpr (PAIRED && one_byte_codes(DST)) {
             if constexpr (DST == ST_P4) CodeIO<DST>::template store8f<LPB / 2>(ot, lbase, j, pk);
             else CodeIO<DST>::template store8<LPB / 2>(ot, lbase, j, qmi, qvi);
         }
+        if (dl != 0u) store_p_lines<C::THREADS, C::TILE>(dt.p, pst, dl);
     } else {
         const MdqDesc od = out_view<SRC, DST>(d);
 #pragma unroll
@@ -1062,6 +1112,7 @@ __global__ __launch_bounds__(Cfg<LOG2B>::THREADS) void mdq_step_kernel(const Mdq
     constexpr bool USE_LUT = (SRC == ST_P4) && C::B >= 32;
     __shared__ float lut_s[USE_LUT ? C::TB * 16 : 1];
     __shared__ int32_t xw_s[6];
+    __shared__ __attribute__((aligned(16))) float pst_s[C::QPL > 0 ? C::TILE : 1];   // staged p stores
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const unsigned grid = gridDim.x, b = blockIdx.x;
@@ -1081,12 +1132,12 @@ __global__ __launch_bounds__(Cfg<LOG2B>::THREADS) void mdq_step_kernel(const Mdq
     ProfAcc pa = {{0, 0, 0, 0, 0}};
     const bool inside = (tl + 1) * C::TILE <= d.numel;
     if (inside && (d.flags & DF_ALIGNED)) {
-        mdq_step_tile<SRC, DST, GT, LOG2B, SR, TILE_VECTOR>(d, tl, lane, wave, lut_s, xw_s, seed, prof_on, pa);
+        mdq_step_tile<SRC, DST, GT, LOG2B, SR, TILE_VECTOR>(d, tl, lane, wave, lut_s, xw_s, pst_s, seed, prof_on, pa);
     } else if (C::QPL > 0 && inside && (d.flags & DF_CODES_ALIGNED)) {
         if constexpr (C::QPL > 0)
-            mdq_step_tile<SRC, DST, GT, LOG2B, SR, TILE_UNALIGNED_PG>(d, tl, lane, wave, lut_s, xw_s, seed, prof_on, pa);
+            mdq_step_tile<SRC, DST, GT, LOG2B, SR, TILE_UNALIGNED_PG>(d, tl, lane, wave, lut_s, xw_s, pst_s, seed, prof_on, pa);
     } else {
-        mdq_step_tile<SRC, DST, GT, LOG2B, SR, TILE_GUARDED>(d, tl, lane, wave, lut_s, xw_s, seed, prof_on, pa);
+        mdq_step_tile<SRC, DST, GT, LOG2B, SR, TILE_GUARDED>(d, tl, lane, wave, lut_s, xw_s, pst_s, seed, prof_on, pa);
     }
     if (prof_on && threadIdx.x == 0) {
 #pragma unroll

@@ -60,11 +60,11 @@ def resync_params(tp, p):
 class Case:
     """One tensor's numpy state (oracle side) and torch state (device side)."""
 
-    def __init__(self, n, B, storage, rng, grad_dtype=np.float32, offset=0, codes_aligned=False):
+    def __init__(self, n, B, storage, rng, grad_dtype=np.float32, offset=0, codes_aligned=False, tail=0):
         self.n, self.B, self.storage = n, B, storage
         self.p = (rng.standard_normal(n) * 0.02).astype(np.float32)
         self.state = list(orc.init_state(n, B, storage))
-        self.offset = offset
+        self.offset, self.tail = offset, tail
         # device copies; `offset` elements of padding in front make the views unaligned (the code
         # arrays too unless `codes_aligned`, as when only params and grads are views of one buffer)
         self.tp = self._dev_view(self.p)
@@ -76,11 +76,20 @@ class Case:
         self.grad_dtype = grad_dtype
 
     def _dev_view(self, a):
-        if self.offset == 0:
+        if self.offset == 0 and self.tail == 0:
             return to_dev(a.copy())
-        buf = np.zeros(a.size + self.offset, dtype=a.dtype)
-        buf[self.offset:] = a
-        return to_dev(buf)[self.offset:]
+        # padding of 7s around the view (the sentinel that padding_intact checks)
+        buf = np.full(a.size + self.offset + self.tail, 7, dtype=a.dtype)
+        buf[self.offset:self.offset + a.size] = a
+        return to_dev(buf)[self.offset:self.offset + a.size]
+
+    def padding_intact(self):
+        base = self.tp._base
+        assert base is not None
+        torch.cuda.synchronize()
+        pad = torch.cat([base[:self.offset], base[self.offset + self.n:]]).cpu()
+        assert pad.numel() == self.offset + self.tail
+        assert torch.equal(pad, torch.full_like(pad, 7.0)), "a store left the params' view"
 
     def grads(self, rng):
         g = (rng.standard_normal(self.n) * 1e-3).astype(np.float32)
@@ -250,6 +259,32 @@ def test_param_and_grad_views_at_odd_offsets(storage, bits, B, offset, gdt):
         p_prev = c.p.copy()
         c.oracle_step(g, step, bits)
         mdq_hip.multi_tensor_step([c.entry(tg, step, bits)], B)
+        c.check(p_prev)
+
+
+@pytest.mark.parametrize("storage,bits", [(orc.STORE_P4, 4), (orc.STORE_S8, 8), (orc.STORE_S16, 16)])
+@pytest.mark.parametrize("B,offset,gdt,full", [(8, 4, np.float32, True), (16, 31, "bf16", False),
+                                               (64, 8, np.float32, True), (128, 16, np.float16, False),
+                                               (256, 28, np.float32, True), (512, 33, "bf16", True),
+                                               (1024, 12, "bf16", True), (1024, 1, np.float32, False),
+                                               (4, 20, np.float32, True)])
+def test_param_views_inside_a_cache_line(storage, bits, B, offset, gdt, full):
+    """Params that start inside a 128-byte line (offset mod 32 elements != 0; offsets that are
+    multiples of 4 keep 16-byte alignment and the vector mode): whole tiles store p line by line
+    through LDS.  Padding before and after the view stays untouched, with the tensor ending on a
+    whole tile (`full`: the last tile is staged too) or on a ragged one."""
+    print(f"case: p line offset={offset} storage={storage} bits={bits} B={B} grad={gdt} full={full}",
+          flush=True)
+    tile = 256 if B == 4 else (1024 if B == 1024 else 512)
+    n = 5 * tile if full else 5 * tile + B // 2 + 3
+    rng = np.random.default_rng(41_000 + 10 * offset + B + storage)
+    c = Case(n, B, storage, rng, grad_dtype=gdt, offset=offset, codes_aligned=True, tail=45)
+    for step in (1, 2):
+        g, tg = c.grads(rng)
+        p_prev = c.p.copy()
+        c.oracle_step(g, step, bits)
+        mdq_hip.multi_tensor_step([c.entry(tg, step, bits)], B)
+        c.padding_intact()
         c.check(p_prev)
 
 
