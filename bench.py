@@ -69,6 +69,8 @@ METRICS = {
     "llama7b": "optimizer params updated/sec + achieved HBM GB/s (% peak), LLaMA-7B shape, 1 GPU",
     "gpt2": "optimizer params updated/sec + achieved HBM GB/s (% peak), GPT-2 small shape, 1 GPU",
     "flat4m": "optimizer params updated/sec, one flat 4,194,304-param tensor (cache-resident), 1 GPU",
+    "config5_views": "optimizer params updated/sec + achieved HBM GB/s (% peak), config 5 sizes as packed "
+                     "param/grad views, 1 GPU",
 }
 
 CONFIGS = {
@@ -79,6 +81,9 @@ CONFIGS = {
     # BASELINE config 1's tensor (59.5 MB of traffic per step: it stays in the 256 MB MALL, so
     # its GB/s is no HBM roofline figure)
     "flat4m": (lambda: [("flat", 4_194_304)], "f32", 4, 128),
+    # BASELINE config 5's 257 ragged sizes with params and grads as views packed back to back
+    # in one buffer (190 of them start inside a 128-byte line), codes and scales separate
+    "config5_views": (lambda: [(f"t{i}", n) for i, n in enumerate(config5_sizes())], "f32", 4, 128),
 }
 
 
@@ -145,23 +150,30 @@ def build_workload(name, dev, seed=0, bits=None):
         k = min(chunk, N - o)
         p[o:o + k].normal_(0.0, 0.02, generator=gen)
         g[o:o + k].copy_(torch.randn(k, device=dev, generator=gen).mul_(1e-3))
+    # params and grads are views packed back to back in one buffer; each tensor's codes start on
+    # a multiple of 256 elements, as separate allocations of the optimizer state would (the same
+    # offsets wherever every size is a multiple of 256, as in the LLaMA and GPT-2 sets)
+    offc = [0]
+    for n in sizes:
+        offc.append(offc[-1] + (n + 255) // 256 * 256)
+    NC = offc[-1]
     if bits == 4:
-        codes = torch.full((N,), 0x08, dtype=torch.uint8, device=dev)   # m code 0, v code 0
+        codes = torch.full((NC,), 0x08, dtype=torch.uint8, device=dev)   # m code 0, v code 0
         vcodes = None
     else:
         mdt, vdt = {8: (torch.int8, torch.uint8), 16: (torch.int16, torch.uint16),
                     32: (torch.int32, torch.uint32)}[bits]
-        codes = torch.zeros(N, dtype=mdt, device=dev)
-        vcodes = torch.zeros(N, dtype=vdt, device=dev)
+        codes = torch.zeros(NC, dtype=mdt, device=dev)
+        vcodes = torch.zeros(NC, dtype=vdt, device=dev)
     sm = torch.zeros(NB, dtype=torch.float32, device=dev)
     sv = torch.zeros(NB, dtype=torch.float32, device=dev)
     vm = torch.full((NB,), -20.0, dtype=torch.float32, device=dev)
     empty = torch.empty(0, dtype=torch.uint8, device=dev)
     entries = []
     o = ob = 0
-    for i, (n, nb) in enumerate(zip(sizes, nbs)):
+    for i, (n, nb, oc) in enumerate(zip(sizes, nbs, offc)):
         entries.append(mdq_hip.TensorState(
-            p[o:o + n], g[o:o + n], codes[o:o + n], empty if vcodes is None else vcodes[o:o + n],
+            p[o:o + n], g[o:o + n], codes[oc:oc + n], empty if vcodes is None else vcodes[oc:oc + n],
             sm[ob:ob + nb], sv[ob:ob + nb], vm[ob:ob + nb],
             1, bits, 1e-3, 0.9, 0.999, 1e-8, 0.01, i))
         o += n
@@ -539,8 +551,8 @@ def profile_summary(args):
                algorithmic_bytes=alg, achieved_gbs=alg / t["avg_ns"], frac_of_peak=alg / t["avg_ns"] / HBM_PEAK_GBS)
     if args.fetch and args.write:
         # the calibration copies are the last three copy dispatches (the workload's set-up may copy too)
-        fk, fc = counter_means(args.fetch, args.kernel), counter_means(args.fetch, "copyBuffer", last=3)
-        wk, wc = counter_means(args.write, args.kernel), counter_means(args.write, "copyBuffer", last=3)
+        fk, fc = counter_means(args.fetch, args.kernel, last=args.pmc_last), counter_means(args.fetch, "copyBuffer", last=3)
+        wk, wc = counter_means(args.write, args.kernel, last=args.pmc_last), counter_means(args.write, "copyBuffer", last=3)
         copy_kib = args.copy_gib * (1 << 30) / 1024.0
         fs, ws = copy_kib / fc["FETCH_SIZE"], copy_kib / wc["WRITE_SIZE"]
         traffic = (fk["FETCH_SIZE"] * fs + wk["WRITE_SIZE"] * ws) * 1024.0
@@ -548,7 +560,7 @@ def profile_summary(args):
                    copy_fetch_kib=fc["FETCH_SIZE"], copy_write_kib=wc["WRITE_SIZE"], fetch_scale=fs, write_scale=ws,
                    traffic_bytes=traffic, traffic_over_algorithmic=traffic / alg)
     if args.sq:
-        sq = counter_means(args.sq, args.kernel)
+        sq = counter_means(args.sq, args.kernel, last=args.pmc_last)
         if "SQ_WAVES" in sq and "SQ_INSTS_VALU" in sq:
             sq["VALU_insts_per_wave"] = sq["SQ_INSTS_VALU"] / sq["SQ_WAVES"]
         out["sq"] = sq
@@ -564,7 +576,10 @@ def profile_summary(args):
            f"Algorithmic bytes per launch {alg:,.0f} -> {out['achieved_gbs']:,.0f} GB/s = "
            f"**{100 * out['frac_of_peak']:.1f} %** of 8 TB/s.", ""]
     if "traffic_bytes" in out:
-        md += ["## HBM traffic (FETCH_SIZE / WRITE_SIZE, KiB per dispatch)", "",
+        md += ["## HBM traffic (FETCH_SIZE / WRITE_SIZE, KiB per dispatch)", ""]
+        if args.pmc_last:
+            md += [f"Counter means over the last {args.pmc_last} dispatches of each counter run.", ""]
+        md += [
                "| | kernel | copy of known size | scale (copy bytes / copy reading) |", "|---|---|---|---|",
                f"| FETCH_SIZE | {out['fetch_kib_per_dispatch']:,.0f} | {out['copy_fetch_kib']:,.0f} | "
                f"{out['fetch_scale']:.4f} |",
@@ -623,6 +638,8 @@ def main():
     ap.add_argument("--sq", help="with --profile-summary: rocprofv3 --pmc SQ_* output directory")
     ap.add_argument("--kernel", default="mdq_step_kernel", help="with --profile-summary: kernel name substring")
     ap.add_argument("--skip", type=int, default=0, help="with --profile-summary: warm-up dispatches to drop")
+    ap.add_argument("--pmc-last", type=int, default=None,
+                    help="with --profile-summary: counter means over the kernel's last N dispatches only")
     ap.add_argument("--grad-stats", action="store_true",
                     help="with --profile-summary: the kernel is the grad-statistics kernel (algorithmic bytes = "
                          "the config's grads, read once)")

@@ -168,6 +168,12 @@ __device__ __forceinline__ vu2 pair_out(uint32_t q0, uint32_t q1, int j)
 // ---------------------------------------------------------------- grad loads
 template <int GT> struct GradIO;
 template <> struct GradIO<GT_F32> {
+    // four grads from LDS at a 4-byte aligned address
+    static __device__ __forceinline__ void lds4(const char *a, float *o) {
+        const float *q = (const float *)a;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) o[c] = q[c];
+    }
     static __device__ __forceinline__ void load4(const void *g, int64_t i, float *o) {
         vf4 v = ld_nt<vf4>(static_cast<const float *>(g) + i);
         o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
@@ -185,6 +191,11 @@ template <> struct GradIO<GT_F32> {
     }
 };
 template <> struct GradIO<GT_BF16> {
+    static __device__ __forceinline__ void lds4(const char *a, float *o) {
+        const uint16_t *q = (const uint16_t *)a;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) o[c] = bits_f((uint32_t)q[c] << 16);
+    }
     static __device__ __forceinline__ void unpack(vu2 v, float *o) {
         o[0] = bits_f(v.x << 16); o[1] = bits_f(v.x & 0xffff0000u);
         o[2] = bits_f(v.y << 16); o[3] = bits_f(v.y & 0xffff0000u);
@@ -203,6 +214,11 @@ template <> struct GradIO<GT_BF16> {
     }
 };
 template <> struct GradIO<GT_F16> {
+    static __device__ __forceinline__ void lds4(const char *a, float *o) {
+        const uint16_t *q = (const uint16_t *)a;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) o[c] = (float)__builtin_bit_cast(_Float16, q[c]);
+    }
     static __device__ __forceinline__ float h2f(uint32_t h) {
         return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
     }
@@ -508,15 +524,59 @@ __device__ __forceinline__ float dequant_m(float code, float sm, float neg8sm)
 
 // ---------------------------------------------------------------- one tile
 // Tile modes.  TILE_VECTOR: every element of the tile lies inside the tensor and
-// all pointers are 16-byte aligned, so vector accesses are used.  TILE_UNALIGNED_PG:
-// the tile lies inside the tensor and the codes are aligned, but p or the grads
-// are not (views at arbitrary element offsets of one buffer, as ZeRO-style flat
-// partitions hand them over): codes move as in TILE_VECTOR, and p and grads are
-// loaded as the same 4-element vectors at element-aligned addresses.  In both
-// modes a p that does not start on a 128-byte line is stored through LDS
-// (store_p_lines).
+// all pointers are 16-byte aligned (p and grads of a one-wave tile on 128-byte
+// lines), so each lane moves its own quads as vectors.  TILE_STAGED (one-wave
+// tiles): the tile lies inside the tensor and the codes are aligned, but p or the
+// grads do not start on a 128-byte line (views at arbitrary element offsets of one
+// buffer, as a flat parameter buffer hands them over).  The lanes' own 16-byte
+// pieces would then split lines between instructions, so p and the grads come in
+// as whole aligned lines straight into LDS (global_load_lds) and p goes out through
+// LDS line by line (store_p_lines); codes move as in TILE_VECTOR.  Config 5 as
+// views back to back, B = 64: 64 % of HBM peak with the lanes' own element-aligned
+// vectors, 80 % staged, level with separate allocations.  TILE_UNALIGNED_PG (the
+// two-wave tiles of B = 1024, and stochastic rounding from B = 128 on, staged_mode):
+// codes as in TILE_VECTOR, p and grads loaded as the lanes' vectors at element-aligned
+// addresses, and p stored through LDS when it does not start on a line.
 // TILE_GUARDED: every access element by element, guarded by idx < numel.
-enum TileMode : int { TILE_GUARDED = 0, TILE_VECTOR = 1, TILE_UNALIGNED_PG = 2 };
+enum TileMode : int { TILE_GUARDED = 0, TILE_VECTOR = 1, TILE_UNALIGNED_PG = 2, TILE_STAGED = 3 };
+
+// Whether tiles with p or grads off their 128-byte lines take TILE_STAGED (else
+// TILE_UNALIGNED_PG).  Same-box A/B on config 5 as packed views, stochastic rounding:
+// staging is faster up to B = 64 (B = 64 8-bit 71.6 -> 75.4 % of HBM peak, B = 32 4-bit
+// 66.0 -> 70.9 %), where each block's span of lanes covers at most one line, and slower
+// from B = 128 on (B = 256 4-bit 79.0 -> 74.0 %), where the Philox work leaves less room
+// for the LDS round trip.  Nearest rounding: faster at every B.
+template <bool SR, int LOG2B>
+constexpr bool staged_mode()
+{
+    return Cfg<LOG2B>::QPL > 0 && Cfg<LOG2B>::WAVES == 1 && (!SR || LOG2B <= 6);
+}
+
+// Bytes of LDS a one-wave staged tile uses for the lines of p (4 B per element) and
+// of the grads (GB B per element), each with one more line for a start inside a line.
+constexpr int staged_lds_bytes(int tile, int gb) { return 4 * tile + 128 + gb * tile + 128; }
+
+// The 128-byte lines that hold src[0 .. NB) (bytes), as aligned 16-byte pieces from
+// the line of src's first byte on, into lds[0 ..) by direct global -> LDS loads
+// (non-temporal; piece w of the lines lands at lds + 16 w).  Lines are 128-byte
+// aligned, so none crosses a page: the bytes around src that they carry lie on
+// pages that src's own bytes map.  One wave; the caller waits (vmcnt) before
+// reading the LDS.
+template <int NB>
+__device__ __forceinline__ void lines_to_lds(const void *src, char *lds, uint32_t off, int lane)
+{
+    const char *l0 = (const char *)src - off;
+    const uint32_t nv = ((off + (uint32_t)NB + 127u) >> 7) * 8u;   // pieces of the covering lines
+    constexpr int R = (NB / 16 + 8 + 63) / 64;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        // the piece of lane l in round r is w = 64 r + l: LDS address = base of the round + 16 l
+        if (64u * r + lane < nv)
+            __builtin_amdgcn_global_load_lds((const MDQ_GLOBAL void *)(l0 + 1024 * r + 16 * lane),
+                                             (__attribute__((address_space(3))) void *)(lds + 1024 * r), 16, 0,
+                                             2 /* nt */);
+    }
+}
 
 // A whole tile's p stores when p does not start on a 128-byte line (pst: TILE floats
 // of LDS, 16-byte aligned, holding the tile's new p; dl = the tile's offset in its
@@ -570,7 +630,14 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
     constexpr bool PAIRED = paired_codes<SRC, DST, LOG2B>();
     constexpr bool FULL = MODE != TILE_GUARDED;           // the whole tile lies inside the tensor
     constexpr bool VEC_PG = MODE == TILE_VECTOR;          // p and grads 16-byte aligned
+    constexpr bool STAGED = MODE == TILE_STAGED;
     static_assert(MODE != TILE_UNALIGNED_PG || C::QPL > 0, "unaligned p/g mode needs 4-element quads");
+    static_assert(!STAGED || (C::QPL > 0 && C::WAVES == 1), "the staged mode is for one-wave tiles of quads");
+    constexpr uint32_t GB = GT == GT_F32 ? 4u : 2u;       // bytes per grad
+    // STAGED: pst holds the lines of p (later the staged p stores), then those of g
+    char *const stp = (char *)pst;
+    char *const stg = (char *)pst + 4 * C::TILE + 128;
+    uint32_t offp = 0, offg = 0;                          // p's / g's byte offset in their first line
 
     unsigned long long t0 = 0;
     if (prof_on) t0 = clock64();
@@ -608,18 +675,26 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
     const uint32_t lbase = (uint32_t)bi * B;
     if constexpr (FULL && C::QPL > 0) {
         const MdqDesc dt = tile_view<SRC, DST, GT>(d, tbase);
+        if constexpr (STAGED) {
+            offp = (uint32_t)reinterpret_cast<uintptr_t>(dt.p) & 127u;
+            offg = (uint32_t)reinterpret_cast<uintptr_t>(dt.g) & 127u;
+            lines_to_lds<4 * C::TILE>(dt.p, stp, offp, lane);
+            lines_to_lds<(int)GB * C::TILE>(dt.g, stg, offg, lane);
+        }
 #pragma unroll
         for (int k = 0; k < C::QPL; ++k) {
             const uint32_t i = lbase + 4 * lane_quad<PAIRED, LOG2B>(j, k);
-            vf4 p4;
-            if constexpr (VEC_PG) {
-                p4 = ld_nt<vf4>(dt.p + i);
-                GradIO<GT>::load4(dt.g, i, gv + 4 * k);
-            } else {
-                p4 = ld_nt_al<vf4, 4>(dt.p + i);
-                GradIO<GT>::load4u(dt.g, i, gv + 4 * k);
+            if constexpr (!STAGED) {
+                vf4 p4;
+                if constexpr (VEC_PG) {
+                    p4 = ld_nt<vf4>(dt.p + i);
+                    GradIO<GT>::load4(dt.g, i, gv + 4 * k);
+                } else {
+                    p4 = ld_nt_al<vf4, 4>(dt.p + i);
+                    GradIO<GT>::load4u(dt.g, i, gv + 4 * k);
+                }
+                pv[4 * k + 0] = p4.x; pv[4 * k + 1] = p4.y; pv[4 * k + 2] = p4.z; pv[4 * k + 3] = p4.w;
             }
-            pv[4 * k + 0] = p4.x; pv[4 * k + 1] = p4.y; pv[4 * k + 2] = p4.z; pv[4 * k + 3] = p4.w;
             if constexpr (!(PAIRED && one_byte_codes(SRC))) CodeIO<SRC>::load4(dt, i, mc + 4 * k, vc + 4 * k);
         }
         if constexpr (PAIRED && one_byte_codes(SRC)) CodeIO<SRC>::template load8<LPB / 2>(dt, lbase, j, mc, vc);
@@ -684,6 +759,20 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         } else {
             __syncthreads();
+        }
+    }
+    if constexpr (STAGED) {
+        // the direct LDS loads count in vmcnt and the compiler does not wait for them
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+        for (int k = 0; k < C::QPL; ++k) {
+            const uint32_t i = lbase + 4 * lane_quad<PAIRED, LOG2B>(j, k);
+            const float *q = (const float *)(stp + offp) + i;
+            pv[4 * k + 0] = q[0]; pv[4 * k + 1] = q[1]; pv[4 * k + 2] = q[2]; pv[4 * k + 3] = q[3];
+            GradIO<GT>::lds4(stg + offg + GB * i, gv + 4 * k);
         }
     }
     if (prof_on) { unsigned long long t = clock64(); pa.c[0] += t - t0; t0 = t; }
@@ -1047,8 +1136,11 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
         const MdqDesc dt = tile_view<SRC, DST, GT>(d, tbase);
         const MdqDesc ot = out_view<SRC, DST>(dt);
         // p's offset in its 128-byte line, in elements (the same for every tile of the
-        // tensor); nonzero: the lanes' p go to LDS and store_p_lines writes them
-        const uint32_t dl = (uint32_t)(reinterpret_cast<uintptr_t>(dt.p) >> 2) & 31u;
+        // tensor); nonzero: the lanes' p go to LDS and store_p_lines writes them.  A
+        // one-wave TILE_VECTOR tile starts on a line.  The LDS reads of p above were
+        // this wave's, issued in order before the writes below.
+        constexpr bool MAY_STAGE = MODE != TILE_VECTOR || C::WAVES > 1;
+        const uint32_t dl = MAY_STAGE ? (uint32_t)(reinterpret_cast<uintptr_t>(dt.p) >> 2) & 31u : 0u;
 #pragma unroll
         for (int k = 0; k < C::QPL; ++k) {
             const uint32_t i = lbase + 4 * lane_quad<PAIRED, LOG2B>(j, k);
@@ -1112,7 +1204,10 @@ __global__ __launch_bounds__(Cfg<LOG2B>::THREADS) void mdq_step_kernel(const Mdq
     constexpr bool USE_LUT = (SRC == ST_P4) && C::B >= 32;
     __shared__ float lut_s[USE_LUT ? C::TB * 16 : 1];
     __shared__ int32_t xw_s[6];
-    __shared__ __attribute__((aligned(16))) float pst_s[C::QPL > 0 ? C::TILE : 1];   // staged p stores
+    // staged tiles: the lines of p and grads, then the p stores (two-wave tiles: the p stores)
+    constexpr int GBK = GT == GT_F32 ? 4 : 2;
+    __shared__ __attribute__((aligned(16)))
+    float pst_s[C::QPL == 0 ? 1 : staged_mode<SR, LOG2B>() ? staged_lds_bytes(C::TILE, GBK) / 4 : C::TILE];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const unsigned grid = gridDim.x, b = blockIdx.x;
@@ -1131,10 +1226,14 @@ __global__ __launch_bounds__(Cfg<LOG2B>::THREADS) void mdq_step_kernel(const Mdq
     const bool prof_on = prof != nullptr && (tile & 63) == 0;
     ProfAcc pa = {{0, 0, 0, 0, 0}};
     const bool inside = (tl + 1) * C::TILE <= d.numel;
-    if (inside && (d.flags & DF_ALIGNED)) {
+    // p and grads on 128-byte lines (tiles start every 2 KB of p, 1 KB of 2-byte grads)
+    const bool lines = ((reinterpret_cast<uintptr_t>(d.p) | reinterpret_cast<uintptr_t>(d.g)) & 127u) == 0;
+    if (inside && (d.flags & DF_ALIGNED) && (C::WAVES > 1 || lines)) {
         mdq_step_tile<SRC, DST, GT, LOG2B, SR, TILE_VECTOR>(d, tl, lane, wave, lut_s, xw_s, pst_s, seed, prof_on, pa);
     } else if (C::QPL > 0 && inside && (d.flags & DF_CODES_ALIGNED)) {
-        if constexpr (C::QPL > 0)
+        if constexpr (staged_mode<SR, LOG2B>())
+            mdq_step_tile<SRC, DST, GT, LOG2B, SR, TILE_STAGED>(d, tl, lane, wave, lut_s, xw_s, pst_s, seed, prof_on, pa);
+        else if constexpr (C::QPL > 0)
             mdq_step_tile<SRC, DST, GT, LOG2B, SR, TILE_UNALIGNED_PG>(d, tl, lane, wave, lut_s, xw_s, pst_s, seed, prof_on, pa);
     } else {
         mdq_step_tile<SRC, DST, GT, LOG2B, SR, TILE_GUARDED>(d, tl, lane, wave, lut_s, xw_s, pst_s, seed, prof_on, pa);

@@ -288,6 +288,25 @@ def test_param_views_inside_a_cache_line(storage, bits, B, offset, gdt, full):
         c.check(p_prev)
 
 
+@pytest.mark.parametrize("storage,bits", [(orc.STORE_P4, 4), (orc.STORE_S8, 8)], ids=["p4", "s8"])
+@pytest.mark.parametrize("B,offset,gdt", [(32, 5, np.float32), (64, 31, "bf16"), (64, 4, np.float16),
+                                          (128, 3, np.float32), (256, 17, "bf16")])
+def test_stochastic_rounding_on_param_views(storage, bits, B, offset, gdt):
+    """Stochastic rounding on params and grads that start inside a 128-byte line (staged lines up
+    to B = 64, the lanes' element-aligned vectors above): codes bit-exact, padding untouched."""
+    print(f"case: stochastic p/g views offset={offset} storage={storage} bits={bits} B={B} grad={gdt}",
+          flush=True)
+    rng = np.random.default_rng(42_000 + 10 * offset + B + storage)
+    c = Case(512 * 6 + B + 5, B, storage, rng, grad_dtype=gdt, offset=offset, codes_aligned=True, tail=37)
+    for step in (1, 2):
+        g, tg = c.grads(rng)
+        p_prev = c.p.copy()
+        c.oracle_step(g, step, bits, rounding=orc.ROUND_STOCHASTIC, seed=99, tensor_id=3)
+        mdq_hip.multi_tensor_step([c.entry(tg, step, bits, tensor_id=3)], B, rounding="stochastic", seed=99)
+        c.padding_intact()
+        c.check(p_prev)
+
+
 @pytest.mark.parametrize("storage,bits", [(orc.STORE_P4, 4), (orc.STORE_S8, 8), (orc.STORE_S16, 16)])
 def test_stochastic_rounding_bit_exact(storage, bits):
     print(f"case: stochastic storage={storage} bits={bits}", flush=True)
