@@ -69,6 +69,7 @@ METRICS = {
     "llama7b": "optimizer params updated/sec + achieved HBM GB/s (% peak), LLaMA-7B shape, 1 GPU",
     "gpt2": "optimizer params updated/sec + achieved HBM GB/s (% peak), GPT-2 small shape, 1 GPU",
     "flat4m": "optimizer params updated/sec, one flat 4,194,304-param tensor (cache-resident), 1 GPU",
+    "config5": "optimizer params updated/sec + achieved HBM GB/s (% peak), config 5 sizes, 1 GPU",
     "config5_views": "optimizer params updated/sec + achieved HBM GB/s (% peak), config 5 sizes as packed "
                      "param/grad views, 1 GPU",
 }
@@ -81,10 +82,14 @@ CONFIGS = {
     # BASELINE config 1's tensor (59.5 MB of traffic per step: it stays in the 256 MB MALL, so
     # its GB/s is no HBM roofline figure)
     "flat4m": (lambda: [("flat", 4_194_304)], "f32", 4, 128),
-    # BASELINE config 5's 257 ragged sizes with params and grads as views packed back to back
-    # in one buffer (190 of them start inside a 128-byte line), codes and scales separate
+    # BASELINE config 5's 257 ragged sizes, each tensor on a 256-element boundary as separate
+    # allocations would be, and with params and grads as views packed back to back in one
+    # buffer (190 of them start inside a 128-byte line), codes and scales separate
+    "config5": (lambda: [(f"t{i}", n) for i, n in enumerate(config5_sizes())], "f32", 4, 128),
     "config5_views": (lambda: [(f"t{i}", n) for i, n in enumerate(config5_sizes())], "f32", 4, 128),
 }
+# configs whose params and grads are views packed back to back (the others: 256-element aligned)
+PACKED_PG = {"config5_views"}
 
 
 def config5_sizes():
@@ -142,21 +147,34 @@ def build_workload(name, dev, seed=0, bits=None):
     NB = sum(nbs)
     gdtype = torch.bfloat16 if gdt == "bf16" else torch.float32
     log(f"workload {name}: {len(sizes)} tensors, {N:,} params, {NB:,} blocks, grads {gdt}")
-    p = torch.empty(N, dtype=torch.float32, device=dev)
-    g = torch.empty(N, dtype=gdtype, device=dev)
-    gen = torch.Generator(device=dev).manual_seed(seed)
-    chunk = 1 << 28
-    for o in range(0, N, chunk):
-        k = min(chunk, N - o)
-        p[o:o + k].normal_(0.0, 0.02, generator=gen)
-        g[o:o + k].copy_(torch.randn(k, device=dev, generator=gen).mul_(1e-3))
-    # params and grads are views packed back to back in one buffer; each tensor's codes start on
-    # a multiple of 256 elements, as separate allocations of the optimizer state would (the same
-    # offsets wherever every size is a multiple of 256, as in the LLaMA and GPT-2 sets)
+    # each tensor's codes start on a multiple of 256 elements, as separate allocations of the
+    # optimizer state would; so do its params and grads, except in PACKED_PG configs, where they
+    # are views packed back to back in one buffer (the same offsets wherever every size is a
+    # multiple of 256, as in the LLaMA and GPT-2 sets)
     offc = [0]
     for n in sizes:
         offc.append(offc[-1] + (n + 255) // 256 * 256)
     NC = offc[-1]
+    offp = [0]
+    for n in sizes:
+        offp.append(offp[-1] + n)
+    if name not in PACKED_PG:
+        offp = offc
+    NP = offp[-1]
+    p = torch.empty(NP, dtype=torch.float32, device=dev)
+    g = torch.zeros(NP, dtype=gdtype, device=dev)
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    if name.startswith("config5"):
+        # BASELINE config 5's grads: heavy tails, zero blocks, outliers
+        p.normal_(0.0, 0.02, generator=gen)
+        for n, op in zip(sizes, offp):
+            g[op:op + n] = config5_grads_device(n, B, gen, dev)
+    else:
+        chunk = 1 << 28
+        for o in range(0, NP, chunk):
+            k = min(chunk, NP - o)
+            p[o:o + k].normal_(0.0, 0.02, generator=gen)
+            g[o:o + k].copy_(torch.randn(k, device=dev, generator=gen).mul_(1e-3))
     if bits == 4:
         codes = torch.full((NC,), 0x08, dtype=torch.uint8, device=dev)   # m code 0, v code 0
         vcodes = None
@@ -170,13 +188,12 @@ def build_workload(name, dev, seed=0, bits=None):
     vm = torch.full((NB,), -20.0, dtype=torch.float32, device=dev)
     empty = torch.empty(0, dtype=torch.uint8, device=dev)
     entries = []
-    o = ob = 0
-    for i, (n, nb, oc) in enumerate(zip(sizes, nbs, offc)):
+    ob = 0
+    for i, (n, nb, op, oc) in enumerate(zip(sizes, nbs, offp, offc)):
         entries.append(mdq_hip.TensorState(
-            p[o:o + n], g[o:o + n], codes[oc:oc + n], empty if vcodes is None else vcodes[oc:oc + n],
+            p[op:op + n], g[op:op + n], codes[oc:oc + n], empty if vcodes is None else vcodes[oc:oc + n],
             sm[ob:ob + nb], sv[ob:ob + nb], vm[ob:ob + nb],
             1, bits, 1e-3, 0.9, 0.999, 1e-8, 0.01, i))
-        o += n
         ob += nb
     plan = mdq_hip.MultiTensorPlan(entries, B)
     return dict(plan=plan, N=N, tensors=len(sizes), B=B, bits=bits, gdt=gdt, entries=entries,
@@ -499,6 +516,29 @@ def trace_stats(trace_dir, kernel, skip):
                 all_avg_ns=sum(durs) / len(durs))
 
 
+def dispatch_table(run_dir, kernel, xcds=8):
+    """Per dispatch of ``kernel``, from one ``rocprofv3 --kernel-trace --pmc GRBM_GUI_ACTIVE
+    SQ_WAVES SQ_INSTS_VALU ...`` run: duration, VALU instructions per wave, and the shader clock
+    the GPU ran at, GRBM_GUI_ACTIVE (busy cycles, summed over the ``xcds`` XCDs) / XCDs / duration.
+    Prints a markdown table."""
+    dur = {}
+    for r in _csv_rows(run_dir, "kernel_trace.csv"):
+        if kernel in r["Kernel_Name"]:
+            dur[_dispatch_key(r)] = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e6
+    cnt = {}
+    for r in _csv_rows(run_dir, "counter_collection.csv"):
+        if kernel in r["Kernel_Name"]:
+            c = cnt.setdefault(_dispatch_key(r), {})
+            c[r["Counter_Name"]] = c.get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+    print("| step | ms | VALU / wave | clock (GHz) |")
+    print("|---|---|---|---|")
+    for i, k in enumerate(sorted(set(dur) & set(cnt))):
+        c, ms = cnt[k], dur[k]
+        valu = c["SQ_INSTS_VALU"] / c["SQ_WAVES"] if c.get("SQ_WAVES") else float("nan")
+        ghz = c.get("GRBM_GUI_ACTIVE", float("nan")) / xcds / (ms * 1e6)
+        print(f"| {i + 1} | {ms:.3f} | {valu:.1f} | {ghz:.2f} |")
+
+
 def counter_means(pmc_dir, kernel, last=None):
     """Mean per dispatch of each counter over the dispatches whose name contains ``kernel`` (only
     the ``last`` of them in dispatch order, when given)."""
@@ -598,7 +638,9 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed steps first (default 3; 50 per point with --sweep-config5, whose sub-ms "
+                         "steps would otherwise time the GPU's clock ramp after a cold start)")
     ap.add_argument("--config", default="llama7b", choices=sorted(CONFIGS))
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--bits", type=int, default=None, choices=(4, 8, 16, 32),
@@ -638,6 +680,9 @@ def main():
     ap.add_argument("--sq", help="with --profile-summary: rocprofv3 --pmc SQ_* output directory")
     ap.add_argument("--kernel", default="mdq_step_kernel", help="with --profile-summary: kernel name substring")
     ap.add_argument("--skip", type=int, default=0, help="with --profile-summary: warm-up dispatches to drop")
+    ap.add_argument("--dispatch-table", metavar="DIR", default=None,
+                    help="per-dispatch duration, VALU per wave and shader clock from one rocprofv3 run "
+                         "with --kernel-trace and --pmc GRBM_GUI_ACTIVE SQ_WAVES SQ_INSTS_VALU (output dir)")
     ap.add_argument("--pmc-last", type=int, default=None,
                     help="with --profile-summary: counter means over the kernel's last N dispatches only")
     ap.add_argument("--grad-stats", action="store_true",
@@ -645,8 +690,13 @@ def main():
                          "the config's grads, read once)")
     ap.add_argument("--cmd", action="append", default=[], help="with --profile-summary: a command to record")
     args = ap.parse_args()
+    if args.warmup is None and not args.sweep_config5:
+        args.warmup = 3
     if args.profile_summary:
         profile_summary(args)
+        return
+    if args.dispatch_table:
+        dispatch_table(args.dispatch_table, args.kernel)
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the step shards by quant block across GPUs "
@@ -659,6 +709,8 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     if args.sweep_config5:
+        if args.warmup is None:
+            args.warmup = 50
         res = sweep_config5(dev, args.steps, args.warmup, packed_views=args.packed_views,
                             view_align=max(1, args.view_align))
         print(json.dumps({"metric": "config 5 sweep: params/s and HBM GB/s per point", "n_gpus": 1,

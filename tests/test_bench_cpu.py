@@ -105,3 +105,28 @@ def test_profile_summary_drops_warmup_and_calibrates_on_the_last_copies(tmp_path
     with open(out + ".md") as f:
         md = f.read()
     assert "average over the 4 timed launches **10.000 ms**" in md
+
+
+def test_dispatch_table_joins_trace_and_counters_by_dispatch(tmp_path):
+    """``--dispatch-table`` on one synthetic rocprofv3 run (kernel trace + counters in one
+    directory): rows follow dispatch order, other kernels are left out, the per-XCD busy
+    cycles divided by the duration give the clock, and counters split over dimension rows add
+    up before dividing."""
+    k = "void mdq::mdq_step_kernel<0, 0, 0, 7, false>(...)"
+    other = "elementwise_kernel"
+    trace = [(k, 3, 0, 1_000_000), (k, 1, 0, 800_000), (other, 2, 0, 5), (k, 4, 0, 500_000)]
+    _write_csv(str(tmp_path / "run" / "a" / "c_kernel_trace.csv"),
+               ["Kernel_Name", "Dispatch_Id", "Start_Timestamp", "End_Timestamp"], trace)
+    cnt = []
+    for disp, ms, ghz, valu in ((1, 0.8, 2.0, 500.0), (3, 1.0, 1.2, 510.0), (4, 0.5, 2.2, 490.0)):
+        busy = ghz * 1e9 * ms * 1e-3 * 8
+        cnt += [(k, disp, "GRBM_GUI_ACTIVE", busy / 2), (k, disp, "GRBM_GUI_ACTIVE", busy / 2),
+                (k, disp, "SQ_WAVES", 100.0), (k, disp, "SQ_INSTS_VALU", valu * 100.0)]
+    cnt.append((other, 2, "SQ_WAVES", 7.0))
+    _write_csv(str(tmp_path / "run" / "a" / "c_counter_collection.csv"),
+               ["Kernel_Name", "Dispatch_Id", "Counter_Name", "Counter_Value"], cnt)
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--dispatch-table", str(tmp_path / "run"),
+                        "--kernel", "mdq_step_kernel"], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    rows = [ln for ln in r.stdout.splitlines() if ln.startswith("| ") and ln[2].isdigit()]
+    assert rows == ["| 1 | 0.800 | 500.0 | 2.00 |", "| 2 | 1.000 | 510.0 | 1.20 |", "| 3 | 0.500 | 490.0 | 2.20 |"]
