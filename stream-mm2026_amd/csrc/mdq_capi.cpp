@@ -169,8 +169,10 @@ int make_desc(const stq_tensor &t, int storage, int grad_dt, int B, MdqDesc &d)
     const int ca = (storage == mdq::ST_S8 || storage == mdq::ST_P4) ? 8 : 4 * cb;
     const bool codes_al = is_aligned(t.exp_avg, ca) && (storage == mdq::ST_P4 || is_aligned(t.exp_avg_sq, ca));
     const bool pg_al = is_aligned(t.p, 16) && is_aligned(t.grad, 4 * gb);
+    const bool pg_lines = is_aligned(t.p, 128) && is_aligned(t.grad, 128);
     // p and grads are always element-aligned (fp32 p, 2- or 4-byte grads): element accesses need no more
-    d.flags = (codes_al ? mdq::DF_CODES_ALIGNED : 0u) | (codes_al && pg_al ? mdq::DF_ALIGNED : 0u);
+    d.flags = (codes_al ? mdq::DF_CODES_ALIGNED : 0u) | (codes_al && pg_al ? mdq::DF_ALIGNED : 0u) |
+              (codes_al && pg_lines ? mdq::DF_LINES : 0u);
     return STQ_OK;
 }
 
@@ -313,25 +315,40 @@ int release_slot(Slot *s, hipStream_t stream)
     return STQ_OK;
 }
 
-// Launches the step kernel of (src_storage -> storage) over the nd
-// descriptors at dd, which the tile starts follow in the same device buffer.
-hipError_t launch_step(const MdqDesc *dd, int nd, int src, int storage, int grad_dt, int log2b, bool sr,
-                       int64_t total_tiles, unsigned long long *prof, uint64_t seed, hipStream_t stream)
+// Whether a launch over these descriptors needs the kernel variant with the staged tile
+// modes: some tensor has whole tiles and aligned codes but p or grads off their 128-byte
+// lines.  Launches without one take the variant that has only the vector and guarded
+// tile modes (same-box A/B, LLaMA-7B 4-bit stochastic: 13.71 ms with the staged modes in
+// the same kernel, 13.48 without).
+bool launch_needs_views(const MdqDesc *descs, size_t n, int log2b)
 {
-    const int grid = 0;   // one workgroup per tile (total_tiles)
+    const int64_t te = mdq::tile_elems(1 << log2b);
+    for (size_t i = 0; i < n; ++i) {
+        const uint32_t f = descs[i].flags;
+        if ((f & mdq::DF_CODES_ALIGNED) && !(f & mdq::DF_LINES) && descs[i].numel >= te) return true;
+    }
+    return false;
+}
+
+// Launches the step kernel of (src_storage -> storage) over the nd
+// descriptors at dd, which the tile starts follow in the same device buffer;
+// one workgroup per tile (total_tiles).
+hipError_t launch_step(const MdqDesc *dd, int nd, int src, int storage, int grad_dt, int log2b, bool sr,
+                       int64_t total_tiles, unsigned long long *prof, uint64_t seed, bool views, hipStream_t stream)
+{
     if (src == storage) {
         switch (storage) {
-        case mdq::ST_P4: return mdq::launch_p4(dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream);
-        case mdq::ST_S8: return mdq::launch_s8(dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream);
-        case mdq::ST_S16: return mdq::launch_s16(dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream);
-        default: return mdq::launch_s32(dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream);
+        case mdq::ST_P4: return mdq::launch_p4(dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, views, stream);
+        case mdq::ST_S8: return mdq::launch_s8(dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, views, stream);
+        case mdq::ST_S16: return mdq::launch_s16(dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, views, stream);
+        default: return mdq::launch_s32(dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, views, stream);
         }
     }
     switch (storage) {
-    case mdq::ST_P4: return mdq::launch_tr_p4(src, dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream);
-    case mdq::ST_S8: return mdq::launch_tr_s8(src, dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream);
-    case mdq::ST_S16: return mdq::launch_tr_s16(src, dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream);
-    default: return mdq::launch_tr_s32(src, dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, grid, stream);
+    case mdq::ST_P4: return mdq::launch_tr_p4(src, dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, views, stream);
+    case mdq::ST_S8: return mdq::launch_tr_s8(src, dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, views, stream);
+    case mdq::ST_S16: return mdq::launch_tr_s16(src, dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, views, stream);
+    default: return mdq::launch_tr_s32(src, dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, views, stream);
     }
 }
 
@@ -359,7 +376,7 @@ int upload_and_launch(const MdqDesc *descs, size_t n, int src_storage, int stora
     rc = upload(ctx, s, need, total_tiles * mdq::tile_elems(1 << log2b), stream);
     if (rc != STQ_OK) return rc;
     const hipError_t e = launch_step(reinterpret_cast<const MdqDesc *>(s.dev), (int)n, src_storage, storage, grad_dt,
-                                     log2b, sr, total_tiles, prof, seed, stream);
+                                     log2b, sr, total_tiles, prof, seed, launch_needs_views(descs, n, log2b), stream);
     if (e != hipSuccess) return hip_fail(e, "kernel launch");
     return release_slot(&s, stream);
 }
@@ -565,7 +582,7 @@ int run_restore(const stq_tensor *tensors, const stq_code_out *out, int n_tensor
         d.code_m = t.exp_avg;
         d.code_v = src == mdq::ST_P4 ? nullptr : t.exp_avg_sq;
         if (!(is_aligned(d.code_m, sca) && (src == mdq::ST_P4 || is_aligned(d.code_v, sca))))
-            d.flags &= ~(mdq::DF_ALIGNED | mdq::DF_CODES_ALIGNED);
+            d.flags &= ~(mdq::DF_ALIGNED | mdq::DF_CODES_ALIGNED | mdq::DF_LINES);
         d.tile_begin = tiles;
         tiles += (t.numel + te - 1) / te;
         d.tile_end = tiles;
@@ -698,7 +715,7 @@ int run_noalloc(const stq_tensor *tensors, int n_tensors, int grad_dt, int ea_dt
     if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(descriptors -> scratch)");
     e = launch_step(reinterpret_cast<const MdqDesc *>(g_scratch_dev[dev]), nd, storage, storage, grad_dt, log2b,
                     rounding == STQ_ROUND_STOCHASTIC, tiles, reinterpret_cast<unsigned long long *>(prof), seed,
-                    stream);
+                    launch_needs_views(descs, (size_t)nd, log2b), stream);
     return e == hipSuccess ? STQ_OK : hip_fail(e, "kernel launch");
 }
 

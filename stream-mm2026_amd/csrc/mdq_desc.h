@@ -15,6 +15,7 @@ enum GradType : int { GT_F32 = 0, GT_BF16 = 1, GT_F16 = 2 };
 enum DescFlags : uint32_t {
     DF_ALIGNED = 1u,        // every pointer meets the vector-access alignment
     DF_CODES_ALIGNED = 2u,  // the code pointers do (p and grads may not)
+    DF_LINES = 4u,          // DF_ALIGNED, and p and grads start on 128-byte lines
 };
 
 struct alignas(16) MdqDesc {

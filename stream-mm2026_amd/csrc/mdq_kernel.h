@@ -619,7 +619,7 @@ __device__ __forceinline__ void store_p_lines(float *p, const float *pst, uint32
     }
 }
 
-template <int SRC, int DST, int GT, int LOG2B, bool SR, int MODE>
+template <int SRC, int DST, int GT, int LOG2B, bool SR, bool VIEWS, int MODE>
 __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int lane, int wave,
                                               float *lut, int32_t *xw, float *pst, unsigned long long seed,
                                               bool prof_on, ProfAcc &pa)
@@ -1139,7 +1139,7 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
         // tensor); nonzero: the lanes' p go to LDS and store_p_lines writes them.  A
         // one-wave TILE_VECTOR tile starts on a line.  The LDS reads of p above were
         // this wave's, issued in order before the writes below.
-        constexpr bool MAY_STAGE = MODE != TILE_VECTOR || C::WAVES > 1;
+        constexpr bool MAY_STAGE = VIEWS && (MODE != TILE_VECTOR || C::WAVES > 1);
         const uint32_t dl = MAY_STAGE ? (uint32_t)(reinterpret_cast<uintptr_t>(dt.p) >> 2) & 31u : 0u;
 #pragma unroll
         for (int k = 0; k < C::QPL; ++k) {
@@ -1187,7 +1187,13 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
 // tile starts, so the ~log2(n_desc) dependent scalar loads hit a few cache
 // lines).  Profiling (prof != null) samples every 64th tile; only the phase
 // ratios of the cycle sums are meaningful.
-template <int SRC, int DST, int GT, int LOG2B, bool SR>
+// VIEWS: the variant with the staged tile modes (and their LDS), which the host
+// launches only when some tensor with whole tiles and aligned codes has p or
+// grads off their 128-byte lines; the other variant has the vector and guarded
+// modes alone, so aligned launches run code without the staged paths' register
+// pressure (LLaMA-7B 4-bit stochastic: 13.71 ms with them in one kernel, 13.36
+// without, same box).
+template <int SRC, int DST, int GT, int LOG2B, bool SR, bool VIEWS>
 __global__ __launch_bounds__(Cfg<LOG2B>::THREADS) void mdq_step_kernel(const MdqDesc *__restrict__ descs,
                                                                       const long long *__restrict__ tile_begin,
                                                                       int n_desc,
@@ -1207,7 +1213,7 @@ __global__ __launch_bounds__(Cfg<LOG2B>::THREADS) void mdq_step_kernel(const Mdq
     // staged tiles: the lines of p and grads, then the p stores (two-wave tiles: the p stores)
     constexpr int GBK = GT == GT_F32 ? 4 : 2;
     __shared__ __attribute__((aligned(16)))
-    float pst_s[C::QPL == 0 ? 1 : staged_mode<SR, LOG2B>() ? staged_lds_bytes(C::TILE, GBK) / 4 : C::TILE];
+    float pst_s[!VIEWS || C::QPL == 0 ? 1 : staged_mode<SR, LOG2B>() ? staged_lds_bytes(C::TILE, GBK) / 4 : C::TILE];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const unsigned grid = gridDim.x, b = blockIdx.x;
@@ -1226,17 +1232,25 @@ __global__ __launch_bounds__(Cfg<LOG2B>::THREADS) void mdq_step_kernel(const Mdq
     const bool prof_on = prof != nullptr && (tile & 63) == 0;
     ProfAcc pa = {{0, 0, 0, 0, 0}};
     const bool inside = (tl + 1) * C::TILE <= d.numel;
-    // p and grads on 128-byte lines (tiles start every 2 KB of p, 1 KB of 2-byte grads)
-    const bool lines = ((reinterpret_cast<uintptr_t>(d.p) | reinterpret_cast<uintptr_t>(d.g)) & 127u) == 0;
-    if (inside && (d.flags & DF_ALIGNED) && (C::WAVES > 1 || lines)) {
-        mdq_step_tile<SRC, DST, GT, LOG2B, SR, TILE_VECTOR>(d, tl, lane, wave, lut_s, xw_s, pst_s, seed, prof_on, pa);
-    } else if (C::QPL > 0 && inside && (d.flags & DF_CODES_ALIGNED)) {
-        if constexpr (staged_mode<SR, LOG2B>())
-            mdq_step_tile<SRC, DST, GT, LOG2B, SR, TILE_STAGED>(d, tl, lane, wave, lut_s, xw_s, pst_s, seed, prof_on, pa);
-        else if constexpr (C::QPL > 0)
-            mdq_step_tile<SRC, DST, GT, LOG2B, SR, TILE_UNALIGNED_PG>(d, tl, lane, wave, lut_s, xw_s, pst_s, seed, prof_on, pa);
+    // DF_LINES: p and grads on 128-byte lines (tiles start every 2 KB of p, 1 KB of 2-byte grads)
+    if constexpr (!VIEWS) {
+        // the host launches this variant only when every tensor with whole tiles and aligned
+        // codes has DF_LINES
+        if (inside && (d.flags & DF_LINES))
+            mdq_step_tile<SRC, DST, GT, LOG2B, SR, false, TILE_VECTOR>(d, tl, lane, wave, lut_s, xw_s, pst_s, seed, prof_on, pa);
+        else
+            mdq_step_tile<SRC, DST, GT, LOG2B, SR, false, TILE_GUARDED>(d, tl, lane, wave, lut_s, xw_s, pst_s, seed, prof_on, pa);
     } else {
-        mdq_step_tile<SRC, DST, GT, LOG2B, SR, TILE_GUARDED>(d, tl, lane, wave, lut_s, xw_s, pst_s, seed, prof_on, pa);
+        if (inside && (d.flags & DF_ALIGNED) && (C::WAVES > 1 || (d.flags & DF_LINES))) {
+            mdq_step_tile<SRC, DST, GT, LOG2B, SR, true, TILE_VECTOR>(d, tl, lane, wave, lut_s, xw_s, pst_s, seed, prof_on, pa);
+        } else if (C::QPL > 0 && inside && (d.flags & DF_CODES_ALIGNED)) {
+            if constexpr (staged_mode<SR, LOG2B>())
+                mdq_step_tile<SRC, DST, GT, LOG2B, SR, true, TILE_STAGED>(d, tl, lane, wave, lut_s, xw_s, pst_s, seed, prof_on, pa);
+            else if constexpr (C::QPL > 0)
+                mdq_step_tile<SRC, DST, GT, LOG2B, SR, true, TILE_UNALIGNED_PG>(d, tl, lane, wave, lut_s, xw_s, pst_s, seed, prof_on, pa);
+        } else {
+            mdq_step_tile<SRC, DST, GT, LOG2B, SR, true, TILE_GUARDED>(d, tl, lane, wave, lut_s, xw_s, pst_s, seed, prof_on, pa);
+        }
     }
     if (prof_on && threadIdx.x == 0) {
 #pragma unroll
