@@ -3,8 +3,9 @@
  *
  * The shared library stream-mm2026_amd/mdq_hip/libstquant_hip.so exports
  * these symbols.  Signatures carry plain pointers, sizes and dtype codes only;
- * every device pointer must address memory of the current HIP device, and
- * every call is asynchronous on the given hipStream_t (NULL = the null stream).
+ * every device pointer must address memory of the current HIP device and be
+ * aligned to its element size (as every torch tensor is), and every call is
+ * asynchronous on the given hipStream_t (NULL = the null stream).
  *
  * Return value: STQ_OK, or an STQ_ERR_* code with a message available from
  * stq_last_error() (thread-local).  Argument errors are reported before any

@@ -134,6 +134,14 @@ int make_desc(const stq_tensor &t, int storage, int grad_dt, int B, MdqDesc &d)
     if (t.numel > 0 && (!t.p || !t.grad || !t.exp_avg || !t.scale_m || !t.scale_v || !t.v_min ||
                         (storage != mdq::ST_P4 && !t.exp_avg_sq)))
         return fail(STQ_ERR_INVALID, "null data pointer");
+    const int gb = grad_dt == STQ_FLOAT ? 4 : 2;
+    const int cb = code_bytes(storage);
+    // Every array must start on a multiple of its element size (torch tensors always do): the
+    // tile modes derive p's and the grads' place in their cache lines from element counts.
+    if (t.numel > 0 && !(is_aligned(t.p, 4) && is_aligned(t.grad, gb) && is_aligned(t.exp_avg, cb) &&
+                         (storage == mdq::ST_P4 || is_aligned(t.exp_avg_sq, cb)) && is_aligned(t.scale_m, 4) &&
+                         is_aligned(t.scale_v, 4) && is_aligned(t.v_min, 4)))
+        return fail(STQ_ERR_INVALID, "data pointers must be aligned to their element size");
 
     std::memset(&d, 0, sizeof d);
     d.p = t.p;
@@ -163,8 +171,6 @@ int make_desc(const stq_tensor &t, int storage, int grad_dt, int B, MdqDesc &d)
     d.step = (uint32_t)t.step;
     d.tensor_id = t.tensor_id;
     d.rng_origin = t.elem_offset;
-    const int gb = grad_dt == STQ_FLOAT ? 4 : 2;
-    const int cb = code_bytes(storage);
     // full tiles move codes in 4-element quads (4 * cb bytes), 1-byte codes in 8-byte pairs
     const int ca = (storage == mdq::ST_S8 || storage == mdq::ST_P4) ? 8 : 4 * cb;
     const bool codes_al = is_aligned(t.exp_avg, ca) && (storage == mdq::ST_P4 || is_aligned(t.exp_avg_sq, ca));

@@ -67,6 +67,20 @@ def test_argument_errors(kw, msg):
     assert msg in err()
 
 
+@pytest.mark.parametrize("which", ["p", "grad", "exp_avg", "exp_avg_sq", "scale_m"])
+def test_pointers_off_their_element_size_are_rejected(which):
+    # int16 / uint16 codes and bf16 grads: p and the scales need 4 bytes, the rest 2
+    L = mdq_hip.lib()
+    ptr = {k: FAKE for k in ("p", "grad", "exp_avg", "exp_avg_sq", "scale_m")}
+    ptr[which] = FAKE + (2 if which in ("p", "scale_m") else 1)
+    rc = L.stq_fused_mdq_adamw(
+        ptr["p"], ptr["grad"], 1, 256, 256, ptr["exp_avg"], 5, 256, ptr["exp_avg_sq"], 6, 256,
+        ptr["scale_m"], 2, FAKE, 2, FAKE, 2, 0.9, 0.999, 1e-3, 0.01, 1e-8, 1, 16, 128,
+        None, 0, 0, 0, 0, None)
+    assert rc == _capi.STQ_ERR_INVALID
+    assert "aligned to their element size" in err()
+
+
 def test_block_size_above_1024_is_clamped_like_the_reference():
     # min(block_size, 1024) (stquant_kernel.cu:421): 4096 -> 1024, so 1 scale suffices for 256
     assert call_single(block=4096, scales=0) == _capi.STQ_ERR_INVALID
