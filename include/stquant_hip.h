@@ -12,9 +12,10 @@
  * device work is queued.
  *
  * The multi-tensor entry points upload a descriptor table per call from
- * staging buffers that later calls reuse, so they refuse (STQ_ERR_INVALID,
- * nothing queued) a stream that is capturing a HIP graph: a replay of such a
- * capture would launch with another call's descriptors.
+ * staging buffers that later calls reuse (or launch from a device copy of an
+ * identical table, see stq_step_table_uploads), so they refuse
+ * (STQ_ERR_INVALID, nothing queued) a stream that is capturing a HIP graph: a
+ * replay of such a capture would launch with another call's descriptors.
  */
 #ifndef STQUANT_HIP_H
 #define STQUANT_HIP_H
@@ -252,6 +253,20 @@ const char *stq_last_error(void);
 
 /* STQ_ABI_VERSION of the loaded library. */
 int stq_abi_version(void);
+
+/*
+ * *count = the number of descriptor tables the step entry points
+ * (stq_fused_mdq_adamw, stq_multi_tensor_mdq_adamw,
+ * stq_multi_tensor_mdq_adamw_restore) have uploaded on the current device
+ * since the library was loaded.  When every tensor of a call has the same step
+ * count and AdamW constants, the step-dependent constants travel as kernel
+ * arguments, so the table of a fixed tensor set stays the same from step to
+ * step; a call whose table equals one that an earlier call on the same stream
+ * left on the device launches from that copy and uploads nothing.  No
+ * reference counterpart: it lets a caller (and the tests) check that steady
+ * steps run without uploads.
+ */
+int stq_step_table_uploads(int64_t *count);
 
 /*
  * Device copies of the step's fp32 math, for checking it against a CPU

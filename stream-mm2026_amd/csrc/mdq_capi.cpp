@@ -190,8 +190,13 @@ struct Slot {
     char *host = nullptr;
     size_t cap = 0;   // bytes
     hipEvent_t done = nullptr;     // recorded behind the slot's last launch
-    hipEvent_t copied = nullptr;   // recorded behind the slot's last upload on the copy stream
+    hipEvent_t copied = nullptr;   // recorded behind the slot's last upload
     bool pending = false;
+    // A step table the device buffer holds (its first table_bytes bytes equal
+    // host[0 .. table_bytes)), uploaded for launches on table_stream; 0 when
+    // the buffer holds anything else.
+    size_t table_bytes = 0;
+    hipStream_t table_stream = nullptr;
 };
 
 struct DevCtx {
@@ -199,6 +204,7 @@ struct DevCtx {
     int cus = 0;
     int next = 0;
     hipStream_t copy_stream = nullptr;   // descriptor uploads (default priority)
+    int64_t table_uploads = 0;           // step tables uploaded (launches without a device copy)
     Slot slots[8];
 };
 
@@ -229,6 +235,7 @@ int take_slot(DevCtx *ctx, size_t need, Slot **out)
 {
     Slot &s = ctx->slots[ctx->next];
     ctx->next = (ctx->next + 1) % 8;
+    s.table_bytes = 0;
     hipError_t e;
     if (s.pending) {
         e = hipEventSynchronize(s.done);
@@ -302,7 +309,9 @@ int upload(DevCtx *ctx, Slot &s, size_t bytes, int64_t elems, hipStream_t stream
     }
     if (on_stream) {
         e = hipMemcpyAsync(s.dev, s.host, bytes, hipMemcpyHostToDevice, stream);
-        return e == hipSuccess ? STQ_OK : hip_fail(e, "hipMemcpyAsync(descriptors)");
+        if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(descriptors)");
+        e = hipEventRecord(s.copied, stream);
+        return e == hipSuccess ? STQ_OK : hip_fail(e, "hipEventRecord");
     }
     e = hipMemcpyAsync(s.dev, s.host, bytes, hipMemcpyHostToDevice, ctx->copy_stream);
     if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(descriptors)");
@@ -340,28 +349,40 @@ bool launch_needs_views(const MdqDesc *descs, size_t n, int log2b)
 // descriptors at dd, which the tile starts follow in the same device buffer;
 // one workgroup per tile (total_tiles).
 hipError_t launch_step(const MdqDesc *dd, int nd, int src, int storage, int grad_dt, int log2b, bool sr,
-                       int64_t total_tiles, unsigned long long *prof, uint64_t seed, bool views, hipStream_t stream)
+                       int64_t total_tiles, unsigned long long *prof, const mdq::StepArgs &sa, bool views,
+                       hipStream_t stream)
 {
     if (src == storage) {
         switch (storage) {
-        case mdq::ST_P4: return mdq::launch_p4(dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, views, stream);
-        case mdq::ST_S8: return mdq::launch_s8(dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, views, stream);
-        case mdq::ST_S16: return mdq::launch_s16(dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, views, stream);
-        default: return mdq::launch_s32(dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, views, stream);
+        case mdq::ST_P4: return mdq::launch_p4(dd, nd, total_tiles, grad_dt, log2b, sr, prof, sa, views, stream);
+        case mdq::ST_S8: return mdq::launch_s8(dd, nd, total_tiles, grad_dt, log2b, sr, prof, sa, views, stream);
+        case mdq::ST_S16: return mdq::launch_s16(dd, nd, total_tiles, grad_dt, log2b, sr, prof, sa, views, stream);
+        default: return mdq::launch_s32(dd, nd, total_tiles, grad_dt, log2b, sr, prof, sa, views, stream);
         }
     }
     switch (storage) {
-    case mdq::ST_P4: return mdq::launch_tr_p4(src, dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, views, stream);
-    case mdq::ST_S8: return mdq::launch_tr_s8(src, dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, views, stream);
-    case mdq::ST_S16: return mdq::launch_tr_s16(src, dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, views, stream);
-    default: return mdq::launch_tr_s32(src, dd, nd, total_tiles, grad_dt, log2b, sr, prof, seed, views, stream);
+    case mdq::ST_P4: return mdq::launch_tr_p4(src, dd, nd, total_tiles, grad_dt, log2b, sr, prof, sa, views, stream);
+    case mdq::ST_S8: return mdq::launch_tr_s8(src, dd, nd, total_tiles, grad_dt, log2b, sr, prof, sa, views, stream);
+    case mdq::ST_S16: return mdq::launch_tr_s16(src, dd, nd, total_tiles, grad_dt, log2b, sr, prof, sa, views, stream);
+    default: return mdq::launch_tr_s32(src, dd, nd, total_tiles, grad_dt, log2b, sr, prof, sa, views, stream);
     }
 }
 
-// Uploads n descriptors to a device slot on `stream` and launches.  The slot's
-// pinned staging buffer is reused only after the event recorded behind its
-// previous launch has completed.  `storage` is the code storage the kernel
-// writes; it reads `src_storage` (the same, except on a storage-changing step).
+// The same bits (so +0 / -0 and NaN patterns count as different).
+bool same_bits(float a, float b) { return std::memcmp(&a, &b, sizeof a) == 0; }
+
+// Launches the step kernel over n descriptors on `stream`.  The table (the
+// descriptors, then their int64 tile starts) goes to the device through a
+// slot of the ring; the slot's pinned staging buffer is reused only after the
+// event recorded behind its previous launch has completed.  When every tensor
+// has the same step_size, inv_sqrt_bc2 and step, those go in the kernel
+// arguments and the table holds 0 in their place, so a fixed tensor set has
+// the same table at every step: a slot whose device buffer already holds it,
+// uploaded for a launch on this stream, is launched from again without an
+// upload (the copy and, for large launches, the wait for the copy stream
+// leave the GPU idle between back-to-back steps).  `storage` is the code
+// storage the kernel writes; it reads `src_storage` (the same, except on a
+// storage-changing step).
 int upload_and_launch(const MdqDesc *descs, size_t n, int src_storage, int storage, int grad_dt, int log2b,
                       bool sr, int64_t total_tiles, unsigned long long *prof, uint64_t seed, hipStream_t stream)
 {
@@ -370,21 +391,61 @@ int upload_and_launch(const MdqDesc *descs, size_t n, int src_storage, int stora
     DevCtx *ctx = nullptr;
     rc = get_ctx(&ctx);
     if (rc != STQ_OK) return rc;
-    std::lock_guard<std::mutex> lk(ctx->mu);
+    mdq::StepArgs sa{seed, 0.0f, 0.0f, 0u, 0u};
+    bool uniform = n > 0;
+    for (size_t i = 1; i < n && uniform; ++i)
+        uniform = same_bits(descs[i].step_size, descs[0].step_size) &&
+                  same_bits(descs[i].inv_sqrt_bc2, descs[0].inv_sqrt_bc2) && descs[i].step == descs[0].step;
+    if (uniform) {
+        sa.step_size = descs[0].step_size;
+        sa.inv_sqrt_bc2 = descs[0].inv_sqrt_bc2;
+        sa.step = descs[0].step;
+        sa.uniform = 1u;
+    }
     const size_t need = n * (sizeof(MdqDesc) + sizeof(long long));
+    thread_local std::vector<char> table;
+    table.resize(need);
+    MdqDesc *td = reinterpret_cast<MdqDesc *>(table.data());
+    std::memcpy(td, descs, n * sizeof(MdqDesc));
+    long long *tb = reinterpret_cast<long long *>(table.data() + n * sizeof(MdqDesc));
+    for (size_t i = 0; i < n; ++i) {
+        tb[i] = descs[i].tile_begin;
+        if (uniform) {
+            td[i].step_size = 0.0f;
+            td[i].inv_sqrt_bc2 = 0.0f;
+            td[i].step = 0u;
+        }
+    }
+    const bool views = launch_needs_views(descs, n, log2b);
+    std::lock_guard<std::mutex> lk(ctx->mu);
     Slot *sp = nullptr;
-    rc = take_slot(ctx, need, &sp);
-    if (rc != STQ_OK) return rc;
-    Slot &s = *sp;
-    std::memcpy(s.host, descs, n * sizeof(MdqDesc));
-    long long *tb = reinterpret_cast<long long *>(s.host + n * sizeof(MdqDesc));
-    for (size_t i = 0; i < n; ++i) tb[i] = descs[i].tile_begin;
-    rc = upload(ctx, s, need, total_tiles * mdq::tile_elems(1 << log2b), stream);
-    if (rc != STQ_OK) return rc;
-    const hipError_t e = launch_step(reinterpret_cast<const MdqDesc *>(s.dev), (int)n, src_storage, storage, grad_dt,
-                                     log2b, sr, total_tiles, prof, seed, launch_needs_views(descs, n, log2b), stream);
+    for (Slot &c : ctx->slots)
+        if (c.table_bytes == need && c.table_stream == stream && std::memcmp(c.host, table.data(), need) == 0) {
+            sp = &c;
+            break;
+        }
+    hipError_t e;
+    if (sp) {
+        // The upload was queued before the launch that last used the slot on this
+        // stream, so it is complete or ahead of this launch in stream order; wait
+        // explicitly only while it is pending (a stream handle can be recycled).
+        e = hipEventQuery(sp->copied);
+        if (e == hipErrorNotReady) e = hipStreamWaitEvent(stream, sp->copied, 0);
+        if (e != hipSuccess) return hip_fail(e, "descriptor table upload");
+    } else {
+        rc = take_slot(ctx, need, &sp);
+        if (rc != STQ_OK) return rc;
+        std::memcpy(sp->host, table.data(), need);
+        rc = upload(ctx, *sp, need, total_tiles * mdq::tile_elems(1 << log2b), stream);
+        if (rc != STQ_OK) return rc;
+        sp->table_bytes = need;
+        sp->table_stream = stream;
+        ++ctx->table_uploads;
+    }
+    e = launch_step(reinterpret_cast<const MdqDesc *>(sp->dev), (int)n, src_storage, storage, grad_dt, log2b, sr,
+                    total_tiles, prof, sa, views, stream);
     if (e != hipSuccess) return hip_fail(e, "kernel launch");
-    return release_slot(&s, stream);
+    return release_slot(sp, stream);
 }
 
 // stq_multi_tensor_grad_stats: descriptors, tile starts and the fp64 partial
@@ -719,8 +780,9 @@ int run_noalloc(const stq_tensor *tensors, int n_tensors, int grad_dt, int ea_dt
     e = hipMemcpyAsync(g_scratch_dev[dev], g_noalloc_stage, (size_t)nd * (sizeof(MdqDesc) + sizeof(long long)),
                        hipMemcpyHostToDevice, stream);
     if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(descriptors -> scratch)");
+    const mdq::StepArgs sa{seed, 0.0f, 0.0f, 0u, 0u};   // every descriptor carries its own step constants
     e = launch_step(reinterpret_cast<const MdqDesc *>(g_scratch_dev[dev]), nd, storage, storage, grad_dt, log2b,
-                    rounding == STQ_ROUND_STOCHASTIC, tiles, reinterpret_cast<unsigned long long *>(prof), seed,
+                    rounding == STQ_ROUND_STOCHASTIC, tiles, reinterpret_cast<unsigned long long *>(prof), sa,
                     launch_needs_views(descs, (size_t)nd, log2b), stream);
     return e == hipSuccess ? STQ_OK : hip_fail(e, "kernel launch");
 }
@@ -806,6 +868,18 @@ int stq_multi_tensor_convert_codes(const stq_code_convert *items, int n_tensors,
 const char *stq_last_error(void) { return g_err.c_str(); }
 
 int stq_abi_version(void) { return STQ_ABI_VERSION; }
+
+int stq_step_table_uploads(int64_t *count)
+{
+    g_err.clear();
+    if (!count) return fail(STQ_ERR_INVALID, "count must not be NULL");
+    DevCtx *ctx = nullptr;
+    const int rc = get_ctx(&ctx);
+    if (rc != STQ_OK) return rc;
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    *count = ctx->table_uploads;
+    return STQ_OK;
+}
 
 int stq_device_math(int which, const float *x, float *y, int64_t n, void *stream)
 {

@@ -53,6 +53,20 @@ struct alignas(16) MdqDesc {
 
 static_assert(sizeof(MdqDesc) % 16 == 0, "descriptor must stay 16-byte sized");
 
+// Kernel arguments of a step launch besides its table: the stochastic-rounding
+// key and, when every tensor of the launch has the same step_size,
+// inv_sqrt_bc2 and step (uniform != 0), those three values.  The descriptors
+// then hold 0 in those fields, so the table of a fixed tensor set is the same
+// at every step and the host can launch again from a device copy it already
+// holds, without an upload.
+struct StepArgs {
+    unsigned long long seed;
+    float step_size;
+    float inv_sqrt_bc2;
+    uint32_t step;
+    uint32_t uniform;
+};
+
 // Tile geometry shared by the host launcher and the kernel: a quant block of
 // B elements is owned by B/EPL lanes (EPL = min(B, 8) elements per lane); a
 // workgroup is one wave, or two for B = 1024, and one tile is one workgroup.

@@ -621,7 +621,7 @@ __device__ __forceinline__ void store_p_lines(float *p, const float *pst, uint32
 
 template <int SRC, int DST, int GT, int LOG2B, bool SR, bool VIEWS, int MODE>
 __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int lane, int wave,
-                                              float *lut, int32_t *xw, float *pst, unsigned long long seed,
+                                              float *lut, int32_t *xw, float *pst, const StepArgs &sa,
                                               bool prof_on, ProfAcc &pa)
 {
     using C = Cfg<LOG2B>;
@@ -641,6 +641,10 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
 
     unsigned long long t0 = 0;
     if (prof_on) t0 = clock64();
+    // the step-dependent constants: kernel arguments when the launch shares them
+    [[maybe_unused]] const uint32_t step_no = sa.uniform ? sa.step : d.step;
+    const float step_size = sa.uniform ? sa.step_size : d.step_size;
+    const float inv_sqrt_bc2 = sa.uniform ? sa.inv_sqrt_bc2 : d.inv_sqrt_bc2;
 
     int bi, j;
     if constexpr (LPB <= 64) { bi = lane / LPB; j = lane % LPB; }
@@ -724,8 +728,8 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
 #pragma unroll
         for (int k = 0; k < C::QPL; ++k) {
             const uint64_t q = (uint64_t)(((base + d.rng_origin) >> 2) + lane_quad<PAIRED, LOG2B>(j, k));
-            const U4 r = mdq_philox4x32_uk<MDQ_SR_ROUNDS>(U4{(uint32_t)q, (uint32_t)(q >> 32), d.tensor_id, d.step},
-                                              (uint32_t)seed, (uint32_t)(seed >> 32));
+            const U4 r = mdq_philox4x32_uk<MDQ_SR_ROUNDS>(U4{(uint32_t)q, (uint32_t)(q >> 32), d.tensor_id, step_no},
+                                              (uint32_t)sa.seed, (uint32_t)(sa.seed >> 32));
             rw[4 * k + 0] = r.x;
             rw[4 * k + 1] = r.y;
             rw[4 * k + 2] = r.z;
@@ -954,8 +958,8 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
                 for (int e = 0; e < EPL; ++e) {
                     const uint64_t idx = (uint64_t)(base + d.rng_origin + e);
                     const uint64_t q = idx >> 2;
-                    U4 r = mdq_philox4x32_uk<MDQ_SR_ROUNDS>(U4{(uint32_t)q, (uint32_t)(q >> 32), d.tensor_id, d.step},
-                                                (uint32_t)seed, (uint32_t)(seed >> 32));
+                    U4 r = mdq_philox4x32_uk<MDQ_SR_ROUNDS>(U4{(uint32_t)q, (uint32_t)(q >> 32), d.tensor_id, step_no},
+                                                (uint32_t)sa.seed, (uint32_t)(sa.seed >> 32));
                     const uint32_t w[4] = {r.x, r.y, r.z, r.w};
                     const uint32_t ww = w[idx & 3];
                     um[e] = mdq_u16_uniform(ww & 0xffffu);
@@ -1127,9 +1131,9 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
     // parameter update with the unquantised m, v (:135-144)
 #pragma unroll
     for (int e = 0; e < EPL; ++e) {
-        const float den = fma_(__builtin_amdgcn_sqrtf(v[e]), d.inv_sqrt_bc2, d.eps);
+        const float den = fma_(__builtin_amdgcn_sqrtf(v[e]), inv_sqrt_bc2, d.eps);
         const float upd = m[e] * __builtin_amdgcn_rcpf(den);
-        pv[e] = fma_(-d.step_size, upd, pv[e] * d.decay);
+        pv[e] = fma_(-step_size, upd, pv[e] * d.decay);
     }
 
     if constexpr (FULL && C::QPL > 0) {
@@ -1198,7 +1202,7 @@ __global__ __launch_bounds__(Cfg<LOG2B>::THREADS) void mdq_step_kernel(const Mdq
                                                                       const long long *__restrict__ tile_begin,
                                                                       int n_desc,
                                                                       unsigned long long *__restrict__ prof,
-                                                                      unsigned long long seed)
+                                                                      const StepArgs sa)
 {
     using C = Cfg<LOG2B>;
     // Occupancy cap at 7 waves per SIMD: the clobber reserves v0..v71, so the
@@ -1237,19 +1241,19 @@ __global__ __launch_bounds__(Cfg<LOG2B>::THREADS) void mdq_step_kernel(const Mdq
         // the host launches this variant only when every tensor with whole tiles and aligned
         // codes has DF_LINES
         if (inside && (d.flags & DF_LINES))
-            mdq_step_tile<SRC, DST, GT, LOG2B, SR, false, TILE_VECTOR>(d, tl, lane, wave, lut_s, xw_s, pst_s, seed, prof_on, pa);
+            mdq_step_tile<SRC, DST, GT, LOG2B, SR, false, TILE_VECTOR>(d, tl, lane, wave, lut_s, xw_s, pst_s, sa, prof_on, pa);
         else
-            mdq_step_tile<SRC, DST, GT, LOG2B, SR, false, TILE_GUARDED>(d, tl, lane, wave, lut_s, xw_s, pst_s, seed, prof_on, pa);
+            mdq_step_tile<SRC, DST, GT, LOG2B, SR, false, TILE_GUARDED>(d, tl, lane, wave, lut_s, xw_s, pst_s, sa, prof_on, pa);
     } else {
         if (inside && (d.flags & DF_ALIGNED) && (C::WAVES > 1 || (d.flags & DF_LINES))) {
-            mdq_step_tile<SRC, DST, GT, LOG2B, SR, true, TILE_VECTOR>(d, tl, lane, wave, lut_s, xw_s, pst_s, seed, prof_on, pa);
+            mdq_step_tile<SRC, DST, GT, LOG2B, SR, true, TILE_VECTOR>(d, tl, lane, wave, lut_s, xw_s, pst_s, sa, prof_on, pa);
         } else if (C::QPL > 0 && inside && (d.flags & DF_CODES_ALIGNED)) {
             if constexpr (staged_mode<SR, LOG2B>())
-                mdq_step_tile<SRC, DST, GT, LOG2B, SR, true, TILE_STAGED>(d, tl, lane, wave, lut_s, xw_s, pst_s, seed, prof_on, pa);
+                mdq_step_tile<SRC, DST, GT, LOG2B, SR, true, TILE_STAGED>(d, tl, lane, wave, lut_s, xw_s, pst_s, sa, prof_on, pa);
             else if constexpr (C::QPL > 0)
-                mdq_step_tile<SRC, DST, GT, LOG2B, SR, true, TILE_UNALIGNED_PG>(d, tl, lane, wave, lut_s, xw_s, pst_s, seed, prof_on, pa);
+                mdq_step_tile<SRC, DST, GT, LOG2B, SR, true, TILE_UNALIGNED_PG>(d, tl, lane, wave, lut_s, xw_s, pst_s, sa, prof_on, pa);
         } else {
-            mdq_step_tile<SRC, DST, GT, LOG2B, SR, true, TILE_GUARDED>(d, tl, lane, wave, lut_s, xw_s, pst_s, seed, prof_on, pa);
+            mdq_step_tile<SRC, DST, GT, LOG2B, SR, true, TILE_GUARDED>(d, tl, lane, wave, lut_s, xw_s, pst_s, sa, prof_on, pa);
         }
     }
     if (prof_on && threadIdx.x == 0) {

@@ -3,8 +3,8 @@
 
 namespace mdq {
 hipError_t launch_tr_s16(int src, const MdqDesc *d, int n, long long tiles, int gt, int log2b, bool sr,
-                       unsigned long long *prof, unsigned long long seed, bool views, hipStream_t s)
+                       unsigned long long *prof, const StepArgs &sa, bool views, hipStream_t s)
 {
-    return launch_tr_to<ST_S16>(src, d, n, tiles, gt, log2b, sr, prof, seed, views, s);
+    return launch_tr_to<ST_S16>(src, d, n, tiles, gt, log2b, sr, prof, sa, views, s);
 }
 }  // namespace mdq

@@ -9,19 +9,19 @@ namespace mdq {
 
 // views: some tensor of the launch has p or grads off their 128-byte lines (and aligned codes),
 // so the launch takes the kernel variant with the staged tile modes.
-hipError_t launch_p4(const MdqDesc *, int, long long, int, int, bool, unsigned long long *, unsigned long long, bool, hipStream_t);
-hipError_t launch_s8(const MdqDesc *, int, long long, int, int, bool, unsigned long long *, unsigned long long, bool, hipStream_t);
-hipError_t launch_s16(const MdqDesc *, int, long long, int, int, bool, unsigned long long *, unsigned long long, bool, hipStream_t);
-hipError_t launch_s32(const MdqDesc *, int, long long, int, int, bool, unsigned long long *, unsigned long long, bool, hipStream_t);
+hipError_t launch_p4(const MdqDesc *, int, long long, int, int, bool, unsigned long long *, const StepArgs &, bool, hipStream_t);
+hipError_t launch_s8(const MdqDesc *, int, long long, int, int, bool, unsigned long long *, const StepArgs &, bool, hipStream_t);
+hipError_t launch_s16(const MdqDesc *, int, long long, int, int, bool, unsigned long long *, const StepArgs &, bool, hipStream_t);
+hipError_t launch_s32(const MdqDesc *, int, long long, int, int, bool, unsigned long long *, const StepArgs &, bool, hipStream_t);
 
 // Storage-changing steps (codes read in storage src, written in the destination
 // storage of the function name): block sizes 2^TRANSITION_LOG2B_MIN ..
 // 2^TRANSITION_LOG2B_MAX; src must differ from the destination.
 constexpr int TRANSITION_LOG2B_MIN = 6, TRANSITION_LOG2B_MAX = 8;
-hipError_t launch_tr_p4(int src, const MdqDesc *, int, long long, int, int, bool, unsigned long long *, unsigned long long, bool, hipStream_t);
-hipError_t launch_tr_s8(int src, const MdqDesc *, int, long long, int, int, bool, unsigned long long *, unsigned long long, bool, hipStream_t);
-hipError_t launch_tr_s16(int src, const MdqDesc *, int, long long, int, int, bool, unsigned long long *, unsigned long long, bool, hipStream_t);
-hipError_t launch_tr_s32(int src, const MdqDesc *, int, long long, int, int, bool, unsigned long long *, unsigned long long, bool, hipStream_t);
+hipError_t launch_tr_p4(int src, const MdqDesc *, int, long long, int, int, bool, unsigned long long *, const StepArgs &, bool, hipStream_t);
+hipError_t launch_tr_s8(int src, const MdqDesc *, int, long long, int, int, bool, unsigned long long *, const StepArgs &, bool, hipStream_t);
+hipError_t launch_tr_s16(int src, const MdqDesc *, int, long long, int, int, bool, unsigned long long *, const StepArgs &, bool, hipStream_t);
+hipError_t launch_tr_s32(int src, const MdqDesc *, int, long long, int, int, bool, unsigned long long *, const StepArgs &, bool, hipStream_t);
 
 hipError_t launch_math(int which, const float *x, float *y, long long n, hipStream_t s);
 hipError_t launch_math_digests(int which, unsigned first, unsigned count, unsigned chunk,

@@ -22,7 +22,7 @@ from .storage import layout_of as storage_of
 __all__ = [
     "ROUND_NEAREST", "ROUND_STOCHASTIC", "STORE_P4", "STORE_S8", "STORE_S16", "STORE_S32",
     "TensorState", "MultiTensorPlan", "fused_step", "multi_tensor_step", "multi_tensor_restore",
-    "RESTORE_BLOCK_SIZES", "grad_stats", "convert_codes", "empty_codes", "storage_of",
+    "RESTORE_BLOCK_SIZES", "grad_stats", "step_table_uploads", "convert_codes", "empty_codes", "storage_of",
     "block_aligned_ranges", "shard_states",
     "device_math", "device_math_digests", "device_log_approx_error", "host_math", "host_round_half_away",
     "host_div_code_range", "host_philox",
@@ -351,6 +351,17 @@ def multi_tensor_restore(entries: Sequence[TensorState], outs, block_size: int, 
             int(block_size), rounding_code(rounding), int(seed) & 0xFFFFFFFFFFFFFFFF, prof_ptr, prof_n,
             _capi.stream_handle(dev))
     check(rc)
+
+
+def step_table_uploads(device=None) -> int:
+    """Descriptor tables the step entry points have uploaded on ``device`` (default: the current
+    CUDA device) since the library was loaded.  Steps over a fixed tensor set whose tensors share
+    their step count and AdamW constants launch from the device copy of an identical table left
+    by an earlier call on the same stream, without an upload."""
+    count = ctypes.c_int64(0)
+    with torch.cuda.device(device if device is not None else torch.cuda.current_device()):
+        check(lib().stq_step_table_uploads(ctypes.byref(count)))
+    return int(count.value)
 
 
 def grad_stats(grads: Sequence[torch.Tensor], out: Optional[torch.Tensor] = None) -> torch.Tensor:

@@ -41,6 +41,7 @@ EXPORTED_SYMBOLS = (
     "stq_multi_tensor_convert_codes",
     "stq_last_error",
     "stq_abi_version",
+    "stq_step_table_uploads",
     "stq_device_math",
     "stq_device_math_digests",
     "stq_device_log_approx_error",
@@ -127,6 +128,8 @@ def lib() -> ctypes.CDLL:
     L.stq_last_error.restype = ctypes.c_char_p
     L.stq_abi_version.argtypes = []
     L.stq_abi_version.restype = ctypes.c_int
+    L.stq_step_table_uploads.argtypes = [vp]
+    L.stq_step_table_uploads.restype = ctypes.c_int
     L.stq_device_math.argtypes = [i32, vp, vp, i64, vp]
     L.stq_device_math.restype = ctypes.c_int
     L.stq_device_math_digests.argtypes = [i32, u32, u32, u32, vp, vp]
