@@ -1,6 +1,7 @@
-"""GPT-2 pretraining with the fused 4-bit optimizer on the GPU (BASELINE config 3 at reduced
-size): stochastic rounding against nearest rounding (the reference's arithmetic, bit-exact to
-the oracle per tests/test_gpu_optimizer.py) on identical seeded batches.
+"""GPT-2 pretraining with the fused 4-bit optimizer on the GPU: stochastic
+rounding against nearest rounding (the reference's arithmetic, bit-exact to the oracle per
+tests/test_gpu_optimizer.py) on identical seeded batches, on a 2-layer model and at the config's
+stated size (the ``test_config3_*`` tests at the end).
 
 - uniform tokens over the full vocabulary (the config's data): loss curves within 1 %;
 - tokens from the first 256 ids (a learnable unigram task whose loss floor is log 256): every
