@@ -126,3 +126,36 @@ def test_ring_slots_taken_in_between():
     torch.cuda.synchronize()
     print(f"uploads over 12 steps: {total}", flush=True)
     assert 1 <= total <= 12
+
+
+def test_random_sequence_of_launches():
+    """A seeded random sequence of 36 launches over three tensor sets (packed 4-bit nearest,
+    int8 stochastic, int16 at 12 bits nearest), on two streams, with per-tensor or shared step
+    counts, grad buffers that move now and then, and grad statistics / conversions in between:
+    every launch exact against the oracle, whatever mix of uploads and device copies it takes."""
+    print("case: random sequence of 36 launches", flush=True)
+    rng = np.random.default_rng(99)
+    sets = [Set(11), Set(12, sizes=[700, 9000], storage=orc.STORE_S8, bits=8),
+            Set(13, sizes=[256, 5000, 128], storage=orc.STORE_S16, bits=12)]
+    rounding = [orc.ROUND_NEAREST, orc.ROUND_STOCHASTIC, orc.ROUND_NEAREST]
+    steps = [0, 0, 0]
+    other = torch.cuda.Stream(DEV)
+    x = torch.randn(10_000, device=DEV)
+    ups = 0
+    for op in range(36):
+        k = int(rng.integers(0, 3))
+        s = sets[k]
+        steps[k] += 1
+        n = len(s.cases)
+        per_tensor = rng.random() < 0.25
+        st = [steps[k] + (3 * i if per_tensor else 0) for i in range(n)]
+        if rng.random() < 0.15:
+            s.tg = [torch.zeros_like(t) for t in s.tg]       # the grads move
+        stream = other if rng.random() < 0.3 else None
+        if stream is None:
+            torch.cuda.current_stream(DEV).wait_stream(other)
+        ups += s.step(st, rounding=rounding[k], seed=40 + k, stream=stream)
+        if rng.random() < 0.2:
+            mdq_hip.grad_stats([x])
+    print(f"uploads over 36 launches: {ups}", flush=True)
+    assert 3 <= ups < 36
