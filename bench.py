@@ -390,10 +390,16 @@ def bit_decision(steps: int):
     return out
 
 
+TRANSITION_WARM = 3   # untimed steady steps before each later transition
+
+
 def transitions(reps: int):
     """Wall time of optimizer steps that change the code storage (first step int16 -> 4-bit
     nibbles, then 4 -> 8 -> 16 -> 4 bits), with the one-launch device conversions and with the
-    reference's per-tensor torch passes, on the GPT-2 small and LLaMA-7B tensor sets."""
+    reference's per-tensor torch passes, on the GPT-2 small and LLaMA-7B tensor sets.  Every
+    transition after the first follows TRANSITION_WARM untimed steady steps at the old width:
+    in training a width changes after many steady steps, on a GPU whose shader clock has
+    settled, while the first steps after a cold start run at a lower clock."""
     import torch
 
     from stquant_opt_fused_io import MDQAdamWSimpleFusedIO
@@ -413,8 +419,10 @@ def transitions(reps: int):
                     params.append(p)
                 opt = MDQAdamWSimpleFusedIO(params, bits=4, block_size=128, sync_timing=False)
                 opt._device_transitions = mode == "device"
-                for label, bits in (("first step 16->4", 4), ("4->8", 8), ("8->16", 16), ("16->4", 4),
-                                    ("steady 4", 4)):
+                for k, (label, bits) in enumerate((("first step 16->4", 4), ("4->8", 8), ("8->16", 16),
+                                                   ("16->4", 4), ("steady 4", 4))):
+                    for _ in range(TRANSITION_WARM if k else 0):
+                        opt.step()                       # steady steps at the current width
                     opt.param_groups[0]["bits"] = bits
                     torch.cuda.synchronize()
                     t0 = time.perf_counter()
