@@ -133,13 +133,14 @@ def bytes_per_param(grad_bytes: int, bits: int, block: int) -> float:
 STORAGE_NAMES = {4: "p4", 8: "s8", 16: "s16", 32: "s32"}
 
 
-def build_workload(name, dev, seed=0, bits=None):
+def build_workload(name, dev, seed=0, bits=None, block=None):
     import torch
 
     import mdq_hip
 
     shapes_fn, gdt, cfg_bits, B = CONFIGS[name]
     bits = cfg_bits if bits is None else bits
+    B = B if block is None else block
     shapes = shapes_fn()
     sizes = [n for _, n in shapes]
     N = sum(sizes)
@@ -654,6 +655,8 @@ def main():
     ap.add_argument("--bits", type=int, default=None, choices=(4, 8, 16, 32),
                     help="code width (canonical storage: packed nibbles, int8/16/32 + uint8/16/32); "
                          "default: the config's (4)")
+    ap.add_argument("--block", type=int, default=None, choices=(64, 128, 256, 512, 1024),
+                    help="quant block size (default: the config's, 128; the reference's drivers pass 256)")
     ap.add_argument("--rounding", default="nearest", choices=("nearest", "stochastic"),
                     help="requant rounding of the timed launches (stochastic: Philox, seed 7)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -738,7 +741,7 @@ def main():
     if args.e2e_gpt2:
         print(json.dumps(e2e_gpt2(args.e2e_steps, args.warmup, args.e2e_out, args.e2e_vocab)), flush=True)
         return
-    w = build_workload(args.config, dev, bits=args.bits)
+    w = build_workload(args.config, dev, bits=args.bits, block=args.block)
     plan = w["plan"]
     if args.rounding == "stochastic":
         import mdq_hip
