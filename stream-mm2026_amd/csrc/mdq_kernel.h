@@ -9,16 +9,17 @@
 // 53-401 (see mdq_step_tile below for the line-by-line map); the layout and
 // schedule are this file's own:
 //
-// * A tile is one wave x EPL elements (EPL = 8 for B >= 8; two waves for
-//   B = 1024), one workgroup per tile.  A quant block of B elements is owned by
+// * A tile is one wave x EPL elements (EPL = 8 for 8 <= B <= 512, 16 for
+//   B = 1024; tile_epl), one workgroup per tile.  A quant block of B elements is owned by
 //   LPB = B/EPL consecutive lanes; lane j of a block owns quads j, j+LPB, ...,
 //   so every 16-lane row reads one contiguous 256-byte span per 16-byte load,
 //   or, when 1-byte codes are involved and LPB is 8, 16 or 32, the permuted
 //   quads of paired_codes below (8-byte code accesses plus one lane swap).
 // * Block reductions (max|m|, max/min log v) run in registers, then across
 //   the LPB lanes with DPP row operations (quad_perm, row_half_mirror,
-//   row_mirror), ds_swizzle for 32 lanes, ds_bpermute for 64, and an LDS
-//   exchange between the two waves of a 1024-element block.  They skip NaN as
+//   row_mirror), ds_swizzle for 32 lanes, ds_bpermute for 64 (and an LDS
+//   exchange between the waves of a block wider than one wave, which the tile
+//   geometry of tile_epl never forms).  They skip NaN as
 //   the reference's fmaxf / fminf trees do, and non-finite quotients give
 //   code 0, as its (int) conversion of NaN does.
 // * A tile whose params do not start on a 128-byte line (views of one buffer)
@@ -47,13 +48,17 @@ namespace mdq {
 // within 2^-24 (1 + 2^-16) of the exact quotient; mdq_vcode_map).
 #define MDQ_VCODE_MAP_ERR 1.3e-7f
 
+// Lanes per block of the paired code layout (paired_codes).
+constexpr bool paired_lpb(int lpb) { return lpb == 8 || lpb == 16 || lpb == 32; }
+
 template <int LOG2B>
 struct Cfg {
     static constexpr int B = 1 << LOG2B;
-    static constexpr int EPL = B >= 8 ? 8 : B;            // elements per lane
+    static constexpr int EPL = tile_epl(B);                // elements per lane
     static constexpr int LPB = B / EPL;                    // lanes per quant block
     static constexpr int QPL = EPL >= 4 ? EPL / 4 : 0;     // 4-element quads per lane
-    static constexpr int WAVES = LPB > 64 ? LPB / 64 : 1;  // waves per workgroup (tile)
+    static constexpr int WAVES = LPB > 64 ? LPB / 64 : 1;  // waves per workgroup (tile); 1 for every B
+    static_assert(!(paired_lpb(LPB) && EPL != 8), "the paired code layout moves two quads per lane");
     static constexpr int THREADS = 64 * WAVES;
     static constexpr int TILE = THREADS * EPL;             // elements per tile
     static constexpr int TB = TILE / B;                    // quant blocks per tile
@@ -114,8 +119,7 @@ constexpr bool paired_codes()
     // same-box A/B against 4-byte quad accesses: packed 4-bit -3.4 %, int8 + uint8 -6 %.
     // Wider codes on the other side of a storage change move as 4-element quads at the
     // same permuted quad positions.
-    return (one_byte_codes(SRC) || one_byte_codes(DST)) &&
-           (Cfg<LOG2B>::LPB == 8 || Cfg<LOG2B>::LPB == 16 || Cfg<LOG2B>::LPB == 32);
+    return (one_byte_codes(SRC) || one_byte_codes(DST)) && paired_lpb(Cfg<LOG2B>::LPB);
 }
 
 // Quad k (0 .. QPL-1) of lane j within its quant block.
@@ -533,8 +537,8 @@ __device__ __forceinline__ float dequant_m(float code, float sm, float neg8sm)
 // as whole aligned lines straight into LDS (global_load_lds) and p goes out through
 // LDS line by line (store_p_lines); codes move as in TILE_VECTOR.  Config 5 as
 // views back to back, B = 64: 64 % of HBM peak with the lanes' own element-aligned
-// vectors, 80 % staged, level with separate allocations.  TILE_UNALIGNED_PG (the
-// two-wave tiles of B = 1024, and stochastic rounding from B = 128 on, staged_mode):
+// vectors, 80 % staged, level with separate allocations.  TILE_UNALIGNED_PG (tiles
+// of more than one wave, and stochastic rounding from B = 128 on, staged_mode):
 // codes as in TILE_VECTOR, p and grads loaded as the lanes' vectors at element-aligned
 // addresses, and p stored through LDS when it does not start on a line.
 // TILE_GUARDED: every access element by element, guarded by idx < numel.
@@ -1214,7 +1218,7 @@ __global__ __launch_bounds__(Cfg<LOG2B>::THREADS) void mdq_step_kernel(const Mdq
     constexpr bool USE_LUT = (SRC == ST_P4) && C::B >= 32;
     __shared__ float lut_s[USE_LUT ? C::TB * 16 : 1];
     __shared__ int32_t xw_s[6];
-    // staged tiles: the lines of p and grads, then the p stores (two-wave tiles: the p stores)
+    // staged tiles: the lines of p and grads, then the p stores (tiles of several waves: the p stores)
     constexpr int GBK = GT == GT_F32 ? 4 : 2;
     __shared__ __attribute__((aligned(16)))
     float pst_s[!VIEWS || C::QPL == 0 ? 1 : staged_mode<SR, LOG2B>() ? staged_lds_bytes(C::TILE, GBK) / 4 : C::TILE];
