@@ -290,7 +290,7 @@ def test_param_views_inside_a_cache_line(storage, bits, B, offset, gdt, full):
 
 @pytest.mark.parametrize("storage,bits", [(orc.STORE_P4, 4), (orc.STORE_S8, 8)], ids=["p4", "s8"])
 @pytest.mark.parametrize("B,offset,gdt", [(32, 5, np.float32), (64, 31, "bf16"), (64, 4, np.float16),
-                                          (128, 3, np.float32), (256, 17, "bf16")])
+                                          (128, 3, np.float32), (256, 17, "bf16"), (1024, 9, np.float32)])
 def test_stochastic_rounding_on_param_views(storage, bits, B, offset, gdt):
     """Stochastic rounding on params and grads that start inside a 128-byte line (staged lines up
     to B = 64, the lanes' element-aligned vectors above): codes bit-exact, padding untouched."""
