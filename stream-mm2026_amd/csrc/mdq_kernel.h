@@ -729,15 +729,34 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
     // wherever a lane owns whole quads).
     uint32_t rw[SR && C::QPL > 0 ? EPL : 1];
     if constexpr (SR && C::QPL > 0) {
+        // The tile's first quad index (workgroup-uniform); a lane's quads lie less than
+        // TILE / 4 above it, so where its low word leaves that much room below 2^32 the high
+        // word is the same for the whole tile and stays in scalar registers (round 0's
+        // first output word and round 1's first product are then scalar work).
+        const uint64_t qt = (uint64_t)((tbase + d.rng_origin) >> 2);
+        if ((uint32_t)qt <= 0xFFFFFFFFu - (uint32_t)(C::TILE / 4)) {
+            const uint32_t qlo = (uint32_t)qt, qhi = (uint32_t)(qt >> 32);
 #pragma unroll
-        for (int k = 0; k < C::QPL; ++k) {
-            const uint64_t q = (uint64_t)(((base + d.rng_origin) >> 2) + lane_quad<PAIRED, LOG2B>(j, k));
-            const U4 r = mdq_philox4x32_uk<MDQ_SR_ROUNDS>(U4{(uint32_t)q, (uint32_t)(q >> 32), d.tensor_id, step_no},
-                                              (uint32_t)sa.seed, (uint32_t)(sa.seed >> 32));
-            rw[4 * k + 0] = r.x;
-            rw[4 * k + 1] = r.y;
-            rw[4 * k + 2] = r.z;
-            rw[4 * k + 3] = r.w;
+            for (int k = 0; k < C::QPL; ++k) {
+                const uint32_t off = (lbase >> 2) + (uint32_t)lane_quad<PAIRED, LOG2B>(j, k);
+                const U4 r = mdq_philox4x32_uk<MDQ_SR_ROUNDS>(U4{qlo + off, qhi, d.tensor_id, step_no},
+                                                  (uint32_t)sa.seed, (uint32_t)(sa.seed >> 32));
+                rw[4 * k + 0] = r.x;
+                rw[4 * k + 1] = r.y;
+                rw[4 * k + 2] = r.z;
+                rw[4 * k + 3] = r.w;
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < C::QPL; ++k) {
+                const uint64_t q = (uint64_t)(((base + d.rng_origin) >> 2) + lane_quad<PAIRED, LOG2B>(j, k));
+                const U4 r = mdq_philox4x32_uk<MDQ_SR_ROUNDS>(U4{(uint32_t)q, (uint32_t)(q >> 32), d.tensor_id, step_no},
+                                                  (uint32_t)sa.seed, (uint32_t)(sa.seed >> 32));
+                rw[4 * k + 0] = r.x;
+                rw[4 * k + 1] = r.y;
+                rw[4 * k + 2] = r.z;
+                rw[4 * k + 3] = r.w;
+            }
         }
     }
     if constexpr (narrows_codes<SRC, DST>()) {

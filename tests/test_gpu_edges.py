@@ -56,3 +56,23 @@ def test_edge_hyper_parameters(storage, bits, rounding):
     before = cases[4].p.copy()
     _run(cases, steps, hps, rounding, bits, 128)
     assert np.array_equal(cases[4].p, before)            # lr = 0: the oracle leaves p as it was
+
+
+@pytest.mark.parametrize("B", [64, 128, 1024])
+def test_stochastic_stream_across_the_2_32_quad_boundary(B):
+    """Pieces whose stochastic-rounding stream starts just below, at and above element 2^34 (quad
+    index 2^32), as a shard of a tensor that large would: the tiles that straddle quad 2^32 draw
+    with a per-lane high counter word, the others with a wave-uniform one; every code bit-exact."""
+    print(f"case: stochastic stream around quad 2^32, B={B}", flush=True)
+    rng = np.random.default_rng(B)
+    n = 3 * 1024 + 77
+    for origin in (2 ** 34 - 2048, 2 ** 34 - B, 2 ** 34, 2 ** 35 - 1024):
+        c = Case(n, B, orc.STORE_P4, rng)
+        for step in (1, 2):
+            g, tg = c.grads(rng)
+            p_prev = c.p.copy()
+            c.oracle_step(g, step, 4, rounding=orc.ROUND_STOCHASTIC, seed=5, tensor_id=9, elem_offset=origin)
+            e = c.entry(tg, step, 4, tensor_id=9)
+            e.elem_offset = origin
+            mdq_hip.multi_tensor_step([e], B, rounding="stochastic", seed=5)
+            c.check(p_prev)
