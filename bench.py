@@ -7,7 +7,11 @@ HBM.  Synthetic data: params ~N(0, 0.02), grads ~N(0, 1e-3), seeded.
 
 Prints ONE JSON line (rank 0): params updated/s, HBM roofline of the kernel
 (algorithmic bytes / HIP-event kernel time) and the CPU oracle timed on a
-bounded slice of the same workload on this host's cores.
+bounded slice of the same workload on this host's cores.  The default run also
+times every other BASELINE config in the same process and reports each under
+``configs`` (config 4 with stochastic rounding, configs 1, 2, 5 -- the last as
+separate allocations and as packed param/grad views -- and config 3's optimizer
+share of a GPT-2 training step); ``--headline-only`` skips them.
 """
 from __future__ import annotations
 
@@ -438,6 +442,127 @@ def transitions(reps: int):
     return out
 
 
+def time_plan(plan, steps: int, warmup: int, step0: int = 0):
+    """``warmup`` untimed launches, then ``steps`` timed ones, each with its step count advanced:
+    wall ms per step (host clock around the launches, bracketed by device synchronisations) and
+    kernel ms per step (HIP events on the stream the library launches on: torch's current one)."""
+    import torch
+
+    step = step0
+    for _ in range(warmup):
+        step += 1
+        plan.set_steps(step)
+        plan.run()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(steps):
+        step += 1
+        plan.set_steps(step)
+        plan.run()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return dict(ms_per_step=wall / steps * 1e3, kernel_ms=ev0.elapsed_time(ev1) / steps, step=step,
+                steps=steps, warmup=warmup)
+
+
+def throughput_record(t, N: int, tensors: int, bits: int, B: int, gdt: str, rounding: str, **extra):
+    """One config's figures from ``time_plan``: params/s on the wall clock, algorithmic HBM GB/s
+    and the fraction of the 8 TB/s peak on the event time."""
+    bpp = bytes_per_param(2 if gdt == "bf16" else 4, bits, B)
+    gbs = bpp * N / (t["kernel_ms"] * 1e-3) / 1e9
+    return dict(params=N, tensors=tensors, bits=bits, block_size=B, grad_dtype=gdt, rounding=rounding,
+                steps=t["steps"], warmup=t["warmup"], ms_per_step=t["ms_per_step"], kernel_ms=t["kernel_ms"],
+                params_per_s=N / (t["ms_per_step"] * 1e-3), bytes_per_param=bpp, hbm_gbs=gbs,
+                frac=gbs / HBM_PEAK_GBS, **extra)
+
+
+def profile_kernel_ms(name: str):
+    """The kernel-trace average (ms) of the committed rocprof summary ``profiles/<name>.json``."""
+    path = os.path.join(ROOT, "profiles", name + ".json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return json.load(f)["avg_ns"] / 1e6
+
+
+def extra_configs(dev, steps: int, llama):
+    """Every other BASELINE config's throughput, measured in the same run as the headline:
+    config 4 with stochastic rounding (on the headline's buffers), config 2 (GPT-2 small set, 100
+    timed steps), config 1 (the flat 4,194,304-param tensor, cache-resident), config 5 over {4, 8}
+    bits x B {64, 128, 256} x {nearest, stochastic} as separate allocations and with params and
+    grads as views packed back to back, and config 3's optimizer share of a GPT-2 training step."""
+    import torch
+
+    import mdq_hip
+
+    out = {}
+    # config 4, stochastic rounding, on the headline's tensors (their state continues)
+    w = llama
+    plan = mdq_hip.MultiTensorPlan(w["entries"], w["B"], rounding="stochastic", seed=7)
+    t = time_plan(plan, steps, 3, step0=w["step"])
+    r = throughput_record(t, w["N"], w["tensors"], w["bits"], w["B"], w["gdt"], "stochastic",
+                          workload="config 4: LLaMA-7B set, stochastic rounding (Philox4x32-7, seed 7)",
+                          profile_kernel_ms=profile_kernel_ms("mdq_step_llama7b_bf16_p4_b128_stochastic"))
+    out["config4_llama7b_stochastic"] = r
+    log(f"config 4 stochastic: {r['kernel_ms']:.3f} ms, {100 * r['frac']:.1f} % of peak")
+    del plan
+    for key, cfg, st, wu, prof in (("config2_gpt2", "gpt2", 100, 10, "mdq_step_gpt2_f32_p4_b128"),
+                                   ("config1_flat4m", "flat4m", 500, 20, None)):
+        w = build_workload(cfg, dev)
+        t = time_plan(w["plan"], st, wu)
+        r = throughput_record(t, w["N"], w["tensors"], w["bits"], w["B"], w["gdt"], "nearest",
+                              workload=f"{cfg}: {w['tensors']} tensors, one multi-tensor launch per step",
+                              profile_kernel_ms=profile_kernel_ms(prof) if prof else None)
+        if cfg == "flat4m":
+            r["note"] = "59.5 MB per step stays in the 256 MB MALL: launch-bound, not an HBM roofline figure"
+        out[key] = r
+        log(f"{key}: {r['ms_per_step']:.4f} ms/step, kernel {r['kernel_ms']:.4f} ms, {100 * r['frac']:.1f} %")
+        del w
+        torch.cuda.empty_cache()
+    for key, views in (("config5", False), ("config5_views", True)):
+        res = sweep_config5(dev, 20, 50, packed_views=views)
+        out[key] = dict(params=res["params"], tensors=res["tensors"], grad_dtype="f32",
+                        layout=("params and grads as views packed back to back in one buffer" if views else
+                                "each tensor on a 1 KiB boundary (separate allocations)"),
+                        points=[dict(bits=p["bits"], block_size=p["block"], rounding=p["rounding"],
+                                     kernel_ms=p["ms"], params_per_s=p["params_per_s"], hbm_gbs=p["gbs"],
+                                     frac=p["pct_peak"] / 100.0, bytes_per_param=p["bytes_per_param"])
+                                for p in res["points"]], steps=20, warmup=50)
+        torch.cuda.empty_cache()
+    try:
+        out["config3_gpt2_e2e"] = e2e_share(30, 5)
+    except ImportError as e:                      # transformers absent: the config cannot run here
+        out["config3_gpt2_e2e"] = {"skipped": f"{type(e).__name__}: {e}"}
+    return out
+
+
+def e2e_share(steps: int, warmup: int):
+    """BASELINE config 3's optimizer share: GPT-2 small (seq 1024, micro-batch 8, bf16 autocast)
+    trained ``steps`` steps on uniform synthetic tokens with the fused 4-bit optimizer
+    (stochastic rounding) and with torch AdamW, the reference harness's timing per phase."""
+    import torch
+
+    import gpt2_pretrain
+
+    res = {}
+    for key, name in (("mdq4_stochastic", "MDQAdamW-Simple-FusedIO"), ("adamw32", "AdamW-32bit")):
+        r = gpt2_pretrain.train(name, steps=steps, warmup=warmup, rounding="stochastic", bits=4)
+        res[key] = {k: r[k] for k in ("Avg_Step_Wall_ms", "Avg_OptimizerStep_ms", "Optimizer_Share_of_Step",
+                                      "Throughput_tokens_per_s", "Optimizer_State_GB", "Avg_Loss")
+                    if k in r}
+        if "Avg_MDQ_FusedKernel_ms" in r:
+            res[key]["Avg_MDQ_FusedKernel_ms"] = r["Avg_MDQ_FusedKernel_ms"]
+        log(f"config 3 {key}: step {r['Avg_Step_Wall_ms']:.1f} ms, optimizer {r['Avg_OptimizerStep_ms']:.3f} ms "
+            f"({100 * r['Optimizer_Share_of_Step']:.2f} %)")
+        torch.cuda.empty_cache()
+    return dict(workload="GPT-2 small, seq 1024, micro-batch 8, bf16 autocast, uniform synthetic tokens",
+                steps=steps, warmup=warmup, **res)
+
+
 def cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -660,6 +785,9 @@ def main():
     ap.add_argument("--rounding", default="nearest", choices=("nearest", "stochastic"),
                     help="requant rounding of the timed launches (stochastic: Philox, seed 7)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--headline-only", action="store_true",
+                    help="time the headline config only (the default run adds every other BASELINE config "
+                         "to the JSON line under 'configs'; profiling commands pass this)")
     ap.add_argument("--sweep-config5", action="store_true",
                     help="time BASELINE config 5 over bits x block x rounding (one JSON line with all points)")
     ap.add_argument("--packed-views", action="store_true",
@@ -759,29 +887,10 @@ def main():
         log(f"shard {args.shard_rank} of {args.shard_of}: {len(mine)} tensor pieces, {w['N']:,} params")
     torch.cuda.synchronize()
 
-    step = 0
-    for _ in range(args.warmup):
-        step += 1
-        plan.set_steps(step)
-        plan.run()
-    torch.cuda.synchronize()
-    log(f"warmup {args.warmup} steps done")
-
-    stream = torch.cuda.current_stream(dev)
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    ev0.record(stream)
-    for _ in range(args.steps):
-        step += 1
-        plan.set_steps(step)
-        plan.run()
-    ev1.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    kernel_ms = ev0.elapsed_time(ev1) / args.steps
-    log(f"timed {args.steps} steps: {kernel_ms:.3f} ms/step (events), wall {wall / args.steps * 1e3:.3f} ms/step")
+    t = time_plan(plan, args.steps, args.warmup)
+    kernel_ms, ms_per_step = t["kernel_ms"], t["ms_per_step"]
+    log(f"timed {args.steps} steps after {args.warmup} warm-up: {kernel_ms:.3f} ms/step (events), "
+        f"wall {ms_per_step:.3f} ms/step")
 
     if args.copy_gib > 0:
         copy_calibration(dev, args.copy_gib)
@@ -790,8 +899,19 @@ def main():
     bpp = bytes_per_param(w["grad_bytes"], w["bits"], w["B"])
     alg_bytes = bpp * N
     achieved = alg_bytes / (kernel_ms * 1e-3) / 1e9
-    ms_per_step = wall / args.steps * 1e3
     value = N / (ms_per_step * 1e-3)
+
+    # the other BASELINE configs, in the default run only (the headline's own command, no
+    # profiling or variant flags)
+    extras = None
+    if (not args.headline_only and args.config == "llama7b" and args.bits is None and args.block is None
+            and args.rounding == "nearest" and shard is None and args.copy_gib == 0):
+        w["step"] = t["step"]
+        del plan
+        extras = extra_configs(dev, args.steps, w)
+        # keep the headline's figures, free its buffers before the CPU baseline
+        w = {k: w[k] for k in ("N", "tensors", "B", "bits", "gdt", "grad_bytes")}
+        torch.cuda.empty_cache()
 
     # HBM bytes per launch measured by rocprofv3 (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0,
     # the factors that map a plain 4 GiB copy's counters to 4 GiB), committed under profiles/
@@ -856,6 +976,8 @@ def main():
         },
         "cpu_baseline": cpu,
     }
+    if extras is not None:
+        out["configs"] = extras
     print(json.dumps(out), flush=True)
 
 

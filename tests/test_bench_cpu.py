@@ -130,3 +130,15 @@ def test_dispatch_table_joins_trace_and_counters_by_dispatch(tmp_path):
     assert r.returncode == 0, r.stderr
     rows = [ln for ln in r.stdout.splitlines() if ln.startswith("| ") and ln[2].isdigit()]
     assert rows == ["| 1 | 0.800 | 500.0 | 2.00 |", "| 2 | 1.000 | 510.0 | 1.20 |", "| 3 | 0.500 | 490.0 | 2.20 |"]
+
+
+def test_throughput_record_divides_the_algorithmic_bytes_by_the_event_time():
+    """Each config's record under ``configs``: params/s on the wall clock, GB/s and the fraction of
+    the 8 TB/s peak from the algorithmic bytes over the HIP-event time."""
+    t = dict(ms_per_step=13.0, kernel_ms=12.5, steps=20, warmup=3, step=23)
+    r = bench.throughput_record(t, 6_738_415_616, 291, 4, 128, "bf16", "stochastic", workload="w")
+    assert r["params_per_s"] == 6_738_415_616 / 13.0e-3
+    alg = 12.1875 * 6_738_415_616
+    assert abs(r["hbm_gbs"] - alg / 12.5e-3 / 1e9) < 1e-9 * r["hbm_gbs"]
+    assert abs(r["frac"] - r["hbm_gbs"] / 8000.0) < 1e-15
+    assert r["rounding"] == "stochastic" and r["workload"] == "w" and r["steps"] == 20
