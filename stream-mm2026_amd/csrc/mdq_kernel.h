@@ -263,17 +263,23 @@ template <> struct CodeIO<ST_P4> {
         mc = (float)(b & 15u);
         vc = b >> 4;
     }
+    // vc receives 4 x the v code: the byte offset of its entry in the block's exp table.
+    // Both nibble fields are masked once per word (the empty asm keeps the masks from being
+    // folded into per-element bit-field extracts), so each element takes one byte-select
+    // conversion (m) and one byte-select add (the table address).
     template <int H>
     static __device__ __forceinline__ void load8(const MdqDesc &d, uint32_t blk_off, int j, float *mc, uint32_t *vc) {
         const vu2 w = ld_nt<vu2>(static_cast<const uint8_t *>(d.code_m) + blk_off + 8 * j);
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const uint32_t q = pair_in<H>(w, j, h);
-            const uint32_t lo = q & 0x0f0f0f0fu;
+            uint32_t lo = q & 0x0f0f0f0fu;
+            uint32_t v4 = (q >> 2) & 0x3c3c3c3cu;
+            asm volatile("" : "+v"(lo), "+v"(v4));
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 mc[4 * h + k] = (float)((lo >> (8 * k)) & 0xffu);
-                vc[4 * h + k] = (q >> (8 * k + 4)) & 15u;
+                vc[4 * h + k] = (v4 >> (8 * k)) & 0xffu;
             }
         }
     }
@@ -635,6 +641,9 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
     constexpr bool FULL = MODE != TILE_GUARDED;           // the whole tile lies inside the tensor
     constexpr bool VEC_PG = MODE == TILE_VECTOR;          // p and grads 16-byte aligned
     constexpr bool STAGED = MODE == TILE_STAGED;
+    // packed codes in the paired layout: vc holds each v code's byte offset in the exp table
+    constexpr bool VC_BYTES = FULL && C::QPL > 0 && PAIRED && SRC == ST_P4;
+    static_assert(!VC_BYTES || USE_LUT, "the paired packed-code load addresses the exp table");
     static_assert(MODE != TILE_UNALIGNED_PG || C::QPL > 0, "unaligned p/g mode needs 4-element quads");
     static_assert(!STAGED || (C::QPL > 0 && C::WAVES == 1), "the staged mode is for one-wave tiles of quads");
     constexpr uint32_t GB = GT == GT_F32 ? 4u : 2u;       // bytes per grad
@@ -834,7 +843,8 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
         for (int e = 0; e < EPL; ++e) {
             const float m0 = dequant_m<SRC>(mc[e], sm, neg8sm);
             float v0;
-            if constexpr (USE_LUT) v0 = lut[bi * 16 + vc[e]];
+            if constexpr (VC_BYTES) v0 = *(const float *)((const char *)(lut + bi * 16) + vc[e]);
+            else if constexpr (USE_LUT) v0 = lut[bi * 16 + vc[e]];
             else v0 = mdq_expf(fma_((float)vc[e], sv, vmin));
             const float g = gv[e];
             m[e] = fma_(d.b1, m0, d.omb1 * g);
@@ -852,14 +862,23 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
     // the requant below).
     constexpr bool FAST_OK = FULL && C::WAVES == 1;
     bool fastv = false;
+    // The lane's largest and smallest x as int32 bit patterns.  A float x satisfies
+    // 1e-12 <= x <= FLT_MAX exactly when its pattern lies in [bits(1e-12), bits(FLT_MAX)]:
+    // +inf and +NaN patterns lie above, negative values, -0 and -NaN (negative as int32)
+    // and values below 1e-12 below.  So the two integer extremes decide the test for all
+    // EPL elements (three-input integer max / min), and on the fast path, where every x is
+    // a positive finite float and floats order as their patterns, they are the lane's
+    // max / min x for the block reductions.
+    int32_t xhi = 0, xlo = 0;
     if constexpr (FAST_OK) {
         if (d.bits <= 8u) {
-            bool good = true;
 #pragma unroll
             for (int e = 0; e < EPL; ++e) {
-                const float x = v[e] + 1e-12f;
-                good = good && x >= 1e-12f && x <= __FLT_MAX__;
+                const int32_t b = __builtin_bit_cast(int32_t, v[e] + 1e-12f);
+                xhi = e == 0 ? b : (b > xhi ? b : xhi);
+                xlo = e == 0 ? b : (b < xlo ? b : xlo);
             }
+            const bool good = xlo >= (int32_t)0x2b8cbcccu && xhi <= (int32_t)0x7f7fffffu;  // 1e-12f, FLT_MAX
             fastv = __builtin_amdgcn_ballot_w64(!good) == 0;
         }
     }
@@ -869,19 +888,15 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
     float amax = 0.0f, lmax = 0.0f, lmin = 0.0f;
     int32_t ka, kx, kn;
     if (fastv) {
-        float xmax = 0.0f, xmin = 0.0f;
 #pragma unroll
         for (int e = 0; e < EPL; ++e) {
             const float a = fabsf(m[e]);
-            const float x = v[e] + 1e-12f;
             amax = e == 0 ? a : fmaxf(amax, a);
-            xmax = e == 0 ? x : fmaxf(xmax, x);
-            xmin = e == 0 ? x : fminf(xmin, x);
         }
         // positive finite floats order as their int32 bit patterns
         ka = __builtin_bit_cast(int32_t, amax);
-        kx = __builtin_bit_cast(int32_t, xmax);
-        kn = __builtin_bit_cast(int32_t, xmin);
+        kx = xhi;
+        kn = xlo;
     } else {
 #pragma unroll
         for (int e = 0; e < EPL; ++e) {
