@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define STQ_ABI_VERSION 2
+#define STQ_ABI_VERSION 3
 
 enum stq_status {
     STQ_OK = 0,
@@ -154,11 +154,12 @@ int stq_multi_tensor_mdq_adamw(const stq_tensor *tensors, int n_tensors,
  * (STQ_NOALLOC_MAX_TENSORS * 184 bytes = 736 KiB, held by every GPU the
  * library runs on until the process ends) and is copied there from a static
  * host buffer with hipMemcpyAsync on `stream`: the host buffer is free again
- * when that call returns (pageable memory), and on the device the copy runs in
- * stream order, after the work queued before it.  All calls on one GPU share
- * the array: calls on the same stream are ordered, but calls on different
- * streams of one GPU race (a later call can overwrite the table an earlier
- * call's kernel is still reading) and must be ordered by the caller.
+ * when that call returns (pageable memory, copied synchronously).  All calls on
+ * one GPU share the array, so each call's copy waits on the device for the
+ * previous call's kernel, on whatever stream it ran (an event created once per
+ * device at the first call): calls on different streams of one GPU are
+ * serialised by the library, each runs on the table it uploaded.  Calls from
+ * several host threads are serialised by a lock.
  */
 int stq_multi_tensor_mdq_adamw_noalloc(const stq_tensor *tensors, int n_tensors,
                                        int grad_dtype, int exp_avg_dtype, int exp_avg_sq_dtype,
@@ -296,6 +297,17 @@ int stq_device_math_digests(int which, uint32_t first, uint32_t count, uint32_t 
  */
 int stq_device_log_approx_error(uint32_t first, uint32_t count, double slope, uint64_t *max_err_bits,
                                 void *stream);
+
+/*
+ * The largest distance, in units in the last place, between the hardware square root
+ * (which = 0, v_sqrt_f32) or reciprocal (which = 1, v_rcp_f32) that the step's
+ * parameter update uses and the correctly rounded result, over the floats with bit
+ * patterns first .. first+count-1 (positive, with positive normal results), atomically
+ * max-ed into the device uint32 *max_ulps (zeroed by the caller).  The parameter
+ * tolerance of the parity tests is derived from this bound (no reference counterpart:
+ * the reference's update uses IEEE sqrtf and division).
+ */
+int stq_device_hw_ulp_error(int which, uint32_t first, uint32_t count, uint32_t *max_ulps, void *stream);
 
 /* Host (CPU) builds of the same inline functions the kernels use. */
 void stq_host_math(int which, const float *x, float *y, int64_t n);

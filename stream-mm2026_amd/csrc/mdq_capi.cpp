@@ -625,6 +625,10 @@ int run_restore(const stq_tensor *tensors, const stq_code_out *out, int n_tensor
             return fail(STQ_ERR_INVALID, "%ssource codes must hold numel (%lld) codes", at.c_str(), (long long)t.numel);
         if (t.numel > 0 && (!t.exp_avg || (src != mdq::ST_P4 && !t.exp_avg_sq)))
             return fail(STQ_ERR_INVALID, "%snull source code pointer", at.c_str());
+        // the source codes are read with element-sized loads: as make_desc requires of the
+        // destination's, each array starts on a multiple of its element size
+        if (t.numel > 0 && !(is_aligned(t.exp_avg, scb) && (src == mdq::ST_P4 || is_aligned(t.exp_avg_sq, scb))))
+            return fail(STQ_ERR_INVALID, "%sdata pointers must be aligned to their element size", at.c_str());
         // the destination arrays are checked as the step's own codes
         stq_tensor td = t;
         td.exp_avg = o.exp_avg;
@@ -735,8 +739,9 @@ static __device__ __align__(256) char scratch[NOALLOC_BYTES];
 
 namespace {
 
-std::mutex g_noalloc_mu;                       // guards the staging buffer and g_scratch_dev
+std::mutex g_noalloc_mu;                       // guards the staging buffer, g_scratch_dev and g_noalloc_done
 char *g_scratch_dev[64] = {nullptr};           // scratch's device address, per device
+hipEvent_t g_noalloc_done[64] = {nullptr};     // recorded behind each call's kernel, per device
 alignas(256) char g_noalloc_stage[NOALLOC_BYTES];
 
 int run_noalloc(const stq_tensor *tensors, int n_tensors, int grad_dt, int ea_dt, int easq_dt, int block_size,
@@ -766,17 +771,28 @@ int run_noalloc(const stq_tensor *tensors, int n_tensors, int grad_dt, int ea_dt
     rc = build_step_descs(tensors, n_tensors, grad_dt, ea_dt, easq_dt, 1 << log2b, descs, &nd, &storage, &tiles);
     if (rc != STQ_OK || nd == 0) return rc;
     if (!g_scratch_dev[dev]) {
-        // once per device, with that device current: its copy of the array
+        // once per device, with that device current: its copy of the array, and the event
+        // that orders each call's table copy after the previous call's kernel
         void *ptr = nullptr;
         e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
         if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+        hipEvent_t ev = nullptr;
+        e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+        if (e != hipSuccess) return hip_fail(e, "hipEventCreateWithFlags(noalloc)");
+        g_noalloc_done[dev] = ev;
         g_scratch_dev[dev] = static_cast<char *>(ptr);
     }
     long long *tb = reinterpret_cast<long long *>(g_noalloc_stage + (size_t)nd * sizeof(MdqDesc));
     for (int i = 0; i < nd; ++i) tb[i] = descs[i].tile_begin;
-    // The staging buffer is pageable memory: hipMemcpyAsync has read it when it returns
-    // (so the next call may refill it), and on the device the copy runs in stream order,
-    // after an earlier call's kernel on this stream has finished reading the table.
+    // Every call on this GPU shares `scratch`: the copy below waits (on the device) for the
+    // kernel of the previous call, on whatever stream it ran, so it never overwrites a table
+    // a kernel is still reading.  Calls on one stream are in stream order anyway.
+    e = hipStreamWaitEvent(stream, g_noalloc_done[dev], 0);
+    if (e != hipSuccess) return hip_fail(e, "hipStreamWaitEvent(noalloc)");
+    // The staging buffer is pageable host memory, and HIP performs a copy from pageable
+    // memory synchronously (hip_runtime_api.h, hipMemcpyAsync: "If host or dst are not
+    // pinned, the memory copy will be performed synchronously"): the buffer has been read
+    // when the call returns, so the next call may refill it.
     e = hipMemcpyAsync(g_scratch_dev[dev], g_noalloc_stage, (size_t)nd * (sizeof(MdqDesc) + sizeof(long long)),
                        hipMemcpyHostToDevice, stream);
     if (e != hipSuccess) return hip_fail(e, "hipMemcpyAsync(descriptors -> scratch)");
@@ -784,7 +800,9 @@ int run_noalloc(const stq_tensor *tensors, int n_tensors, int grad_dt, int ea_dt
     e = launch_step(reinterpret_cast<const MdqDesc *>(g_scratch_dev[dev]), nd, storage, storage, grad_dt, log2b,
                     rounding == STQ_ROUND_STOCHASTIC, tiles, reinterpret_cast<unsigned long long *>(prof), sa,
                     launch_needs_views(descs, (size_t)nd, log2b), stream);
-    return e == hipSuccess ? STQ_OK : hip_fail(e, "kernel launch");
+    if (e != hipSuccess) return hip_fail(e, "kernel launch");
+    e = hipEventRecord(g_noalloc_done[dev], stream);
+    return e == hipSuccess ? STQ_OK : hip_fail(e, "hipEventRecord(noalloc)");
 }
 
 }  // namespace
@@ -902,6 +920,16 @@ int stq_device_log_approx_error(uint32_t first, uint32_t count, double slope, ui
                                               reinterpret_cast<unsigned long long *>(max_err_bits),
                                               reinterpret_cast<hipStream_t>(stream));
     return e == hipSuccess ? STQ_OK : hip_fail(e, "log error kernel launch");
+}
+
+int stq_device_hw_ulp_error(int which, uint32_t first, uint32_t count, uint32_t *max_ulps, void *stream)
+{
+    g_err.clear();
+    if (which != 0 && which != 1) return fail(STQ_ERR_INVALID, "which must be 0 (sqrt) or 1 (reciprocal)");
+    if ((uint64_t)first + count > 0x100000000ull) return fail(STQ_ERR_INVALID, "range exceeds 2^32");
+    if (count > 0 && !max_ulps) return fail(STQ_ERR_INVALID, "null output");
+    hipError_t e = mdq::launch_hw_ulp_err(which, first, count, max_ulps, reinterpret_cast<hipStream_t>(stream));
+    return e == hipSuccess ? STQ_OK : hip_fail(e, "hardware ulp error kernel launch");
 }
 
 int stq_device_math_digests(int which, uint32_t first, uint32_t count, uint32_t chunk, uint64_t *digests,

@@ -28,5 +28,6 @@ hipError_t launch_math_digests(int which, unsigned first, unsigned count, unsign
                                unsigned long long *dig, hipStream_t s);
 hipError_t launch_log_approx_err(unsigned first, unsigned count, double slope, unsigned long long *out,
                                  hipStream_t s);
+hipError_t launch_hw_ulp_err(int which, unsigned first, unsigned count, unsigned *out, hipStream_t s);
 
 }  // namespace mdq

@@ -79,6 +79,43 @@ __global__ __launch_bounds__(256) void log_approx_err_kernel(unsigned first, uns
     if ((threadIdx.x & 63) == 0) atomicMax(out, (unsigned long long)__double_as_longlong(m));
 }
 
+// The largest distance in units in the last place between the hardware square root
+// (which = 0) or reciprocal (which = 1) the step's parameter update uses and the
+// correctly rounded result, over x = bits_f(first .. first+count-1) (positive floats
+// whose result is a positive normal float).  The correctly rounded result is the fp64
+// operation (correctly rounded) rounded to fp32: rounding twice is exact for sqrt and
+// division when the wider format has at least 2p + 2 bits (53 >= 2 * 24 + 2), so it
+// equals IEEE sqrtf / 1.0f / x.
+__global__ __launch_bounds__(256) void hw_ulp_err_kernel(int which, unsigned first, unsigned count,
+                                                         unsigned *__restrict__ out)
+{
+    unsigned m = 0;
+    for (unsigned long long i = (unsigned long long)blockIdx.x * blockDim.x + threadIdx.x; i < count;
+         i += (unsigned long long)gridDim.x * blockDim.x) {
+        const float x = bits_f(first + (unsigned)i);
+        const float hw = which == 0 ? __builtin_amdgcn_sqrtf(x) : __builtin_amdgcn_rcpf(x);
+        const float rn = which == 0 ? (float)__builtin_sqrt((double)x) : (float)(1.0 / (double)x);
+        const unsigned a = f_bits(hw), b = f_bits(rn);
+        const unsigned d = a > b ? a - b : b - a;
+        m = d > m ? d : m;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const unsigned o = (unsigned)__shfl_xor((int)m, off, 64);
+        m = o > m ? o : m;
+    }
+    if ((threadIdx.x & 63) == 0) atomicMax(out, m);
+}
+
+hipError_t launch_hw_ulp_err(int which, unsigned first, unsigned count, unsigned *out, hipStream_t s)
+{
+    if (count == 0) return hipSuccess;
+    unsigned long long blocks = ((unsigned long long)count + 255) / 256;
+    int grid = (int)(blocks < 65536 ? blocks : 65536);
+    hipLaunchKernelGGL(hw_ulp_err_kernel, dim3(grid), dim3(256), 0, s, which, first, count, out);
+    return hipGetLastError();
+}
+
 hipError_t launch_log_approx_err(unsigned first, unsigned count, double slope, unsigned long long *out,
                                  hipStream_t s)
 {

@@ -45,6 +45,7 @@ EXPORTED_SYMBOLS = (
     "stq_device_math",
     "stq_device_math_digests",
     "stq_device_log_approx_error",
+    "stq_device_hw_ulp_error",
     "stq_host_math",
     "stq_host_round_half_away",
     "stq_host_div_code_range",
@@ -53,7 +54,7 @@ EXPORTED_SYMBOLS = (
 
 
 # STQ_ABI_VERSION of include/stquant_hip.h this package is written against
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 
 class StqTensor(ctypes.Structure):
@@ -136,6 +137,8 @@ def lib() -> ctypes.CDLL:
     L.stq_device_math_digests.restype = ctypes.c_int
     L.stq_device_log_approx_error.argtypes = [u32, u32, ctypes.c_double, vp, vp]
     L.stq_device_log_approx_error.restype = ctypes.c_int
+    L.stq_device_hw_ulp_error.argtypes = [i32, u32, u32, vp, vp]
+    L.stq_device_hw_ulp_error.restype = ctypes.c_int
     L.stq_host_math.argtypes = [i32, vp, vp, i64]
     L.stq_host_math.restype = None
     L.stq_host_round_half_away.argtypes = [vp, vp, vp, i64, i32]

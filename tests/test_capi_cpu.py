@@ -27,7 +27,7 @@ def test_exports_every_declared_symbol():
     for name in names:
         assert hasattr(L, name), name
     assert set(names) == set(_capi.EXPORTED_SYMBOLS)
-    assert L.stq_abi_version() == _capi.ABI_VERSION == 2
+    assert L.stq_abi_version() == _capi.ABI_VERSION == 3
 
 
 FAKE = 0x1000  # never dereferenced: every call below fails argument checks first
@@ -171,6 +171,10 @@ def call_restore(src=2, dst=0, bits=4, block=128, numel=256, src_m=FAKE, src_v=F
     (dict(dst_n=100), "packed4: exp_avg numel must match parameters"),
     (dict(dst_m=FAKE + 4096 + 100), "source and destination codes overlap"),
     (dict(src=5), "storage must be STQ_STORE_P4 .. STQ_STORE_S32"),
+    # int16 / int32 source codes are read with element-sized loads
+    (dict(src=2, src_m=FAKE + 1), "data pointers must be aligned to their element size"),
+    (dict(src=2, src_v=FAKE + 4096 + 1), "data pointers must be aligned to their element size"),
+    (dict(src=3, src_m=FAKE + 2), "data pointers must be aligned to their element size"),
 ])
 def test_restore_argument_errors(kw, msg):
     assert call_restore(**kw) == _capi.STQ_ERR_INVALID

@@ -2,7 +2,8 @@
 C implementation: bit-identical on every input of their domain, checked via
 per-chunk digests over all 2^31 - 2^23 positive normals (log) and all 2^32
 bit patterns (exp), plus an elementwise pass.  The stochastic requant's
-reciprocal (mdq_rcp_rn) against IEEE division on every positive normal below 2^126."""
+reciprocal (mdq_rcp_rn) against IEEE division on every positive normal below 2^126; the hardware
+sqrt and reciprocal of the parameter update within 1 ulp of IEEE on their normal range."""
 import os
 import re
 
@@ -92,3 +93,18 @@ def test_vcode_map_is_within_half_an_ulp():
     assert rel0.max() <= bound, (rel0.max(), dv[nz][rel0.argmax()], vmin[nz][rel0.argmax()])
     assert np.all(y[~nz, 1] == 0.0)
     print(f"vcode map: max rel error c1 {rel1.max():.3e}, c0 {rel0.max():.3e} (bound {bound:.3e})", flush=True)
+
+
+@pytest.mark.parametrize("which,first,count", [
+    ("sqrt", 0x00800000, 0x7F800000 - 0x00800000),       # every positive normal
+    ("rcp", 0x00800000, 0x7E800000 - 0x00800000),        # every positive normal below 2^126
+])
+def test_hardware_sqrt_and_reciprocal_within_one_ulp(which, first, count):
+    """The step kernel's parameter update takes v_sqrt_f32 and v_rcp_f32 where the reference
+    (and the oracle) take IEEE sqrtf and division; the parameter bar of the parity tests
+    (tests/param_bar.py) is derived from each being within 1 ulp of the correctly rounded result.
+    Checked on every float of the update's normal range (the device's fp64 sqrt / division
+    rounded to fp32 is the correctly rounded result)."""
+    ulps = mdq_hip.device_hw_ulp_error(which, first, count)
+    print(f"{which}: max {ulps} ulp from the correctly rounded result over {count:,} floats", flush=True)
+    assert ulps <= 1

@@ -3,7 +3,11 @@ multi-tensor entry point (stq_multi_tensor_mdq_adamw), through the C ABI: the sa
 stepped by each from identical states give bit-identical codes, scales and params.  Two calls in
 a row, the second with fewer and smaller tensors (the fixed descriptor array keeps the first
 call's table, which the second must not read); nearest and stochastic rounding, packed 4-bit and
-int8 codes.  A list longer than STQ_NOALLOC_MAX_TENSORS is refused before any device work."""
+int8 codes.  Calls queued back to back with no synchronisation between them, the first long
+enough that its kernel still runs when the second call's table is copied, on one stream and
+alternating between two streams (every call on a GPU shares the one descriptor array, so the
+library orders each copy after the previous call's kernel).  A list longer than
+STQ_NOALLOC_MAX_TENSORS is refused before any device work."""
 import numpy as np
 import pytest
 import torch
@@ -69,3 +73,63 @@ def test_noalloc_refuses_too_many_tensors():
     torch.cuda.synchronize()
     for x, y in zip(ts[0], before):
         assert torch.equal(x.view(torch.uint8), y.view(torch.uint8))
+
+
+def _assert_same(ref, got, what):
+    for i, (a, b) in enumerate(zip(ref, got)):
+        for name, x, y in zip(("p", "grad", "exp_avg", "exp_avg_sq", "scale_m", "scale_v", "v_min"), a, b):
+            assert torch.equal(x.view(torch.uint8), y.view(torch.uint8)), (what, i, name)
+
+
+@pytest.mark.parametrize("rounding", ["nearest", "stochastic"])
+def test_noalloc_calls_back_to_back_without_a_sync(rounding):
+    """A large set (four 2^24-element tensors) then a small one, queued on one stream with no
+    synchronisation in between: the second table copy must wait for the first kernel.  The
+    ordinary entry point steps identical copies; the noalloc calls upload nothing to its ring."""
+    print(f"case: noalloc back to back on one stream, {rounding}", flush=True)
+    big = [1 << 24] * 4 + [12_345]
+    small = [700, 5, 65_536]
+    ref_a, got_a = make_set(big, 4, 21)
+    ref_b, got_b = make_set(small, 4, 22)
+    mdq_hip.MultiTensorPlan(entries(ref_a, 4, 3), B, rounding=rounding, seed=5).run()
+    mdq_hip.MultiTensorPlan(entries(ref_b, 4, 4), B, rounding=rounding, seed=5).run()
+    plan_a = mdq_hip.MultiTensorPlan(entries(got_a, 4, 3), B, rounding=rounding, seed=5)
+    plan_b = mdq_hip.MultiTensorPlan(entries(got_b, 4, 4), B, rounding=rounding, seed=5)
+    torch.cuda.synchronize()
+    before = mdq_hip.step_table_uploads()
+    plan_a.run(noalloc=True)
+    plan_b.run(noalloc=True)
+    after = mdq_hip.step_table_uploads()
+    torch.cuda.synchronize()
+    assert after == before, "the noalloc calls must not take the ordinary entry point's ring"
+    _assert_same(ref_a, got_a, "large set")
+    _assert_same(ref_b, got_b, "small set")
+    print(f"{sum(big):,} then {sum(small):,} params bit-identical, uploads {before} -> {after}", flush=True)
+
+
+def test_noalloc_calls_alternating_between_two_streams():
+    """Two tensor sets of identical shapes, one per stream, stepped alternately for four steps
+    with no synchronisation: a kernel that read the other stream's table would step the other
+    set (valid memory, wrong result).  Both sets must equal the ordinary entry point's steps."""
+    print("case: noalloc alternating between two streams", flush=True)
+    sizes = [1 << 23, 1 << 23, 33_333, 129]
+    ref_a, got_a = make_set(sizes, 8, 31)
+    ref_b, got_b = make_set(sizes, 8, 32)
+    for step in range(1, 5):
+        for ref in (ref_a, ref_b):
+            mdq_hip.MultiTensorPlan(entries(ref, 8, step), B, rounding="stochastic", seed=9).run()
+    torch.cuda.synchronize()
+    s1, s2 = torch.cuda.Stream(DEV), torch.cuda.Stream(DEV)
+    s1.wait_stream(torch.cuda.current_stream(DEV))
+    s2.wait_stream(torch.cuda.current_stream(DEV))
+    plans = [(s1, mdq_hip.MultiTensorPlan(entries(got_a, 8, 1), B, rounding="stochastic", seed=9)),
+             (s2, mdq_hip.MultiTensorPlan(entries(got_b, 8, 1), B, rounding="stochastic", seed=9))]
+    for step in range(1, 5):
+        for stream, plan in plans:
+            plan.set_steps(step)
+            with torch.cuda.stream(stream):
+                plan.run(noalloc=True)
+    torch.cuda.synchronize()
+    _assert_same(ref_a, got_a, "stream 1 set")
+    _assert_same(ref_b, got_b, "stream 2 set")
+    print(f"2 x {sum(sizes):,} params, 4 alternating steps bit-identical", flush=True)
