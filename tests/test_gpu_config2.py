@@ -64,7 +64,7 @@ def test_gpt2_small_set_three_steps_every_tensor():
             assert_bits_equal(f"{tag} scale_m", sm[c:d], hsm)
             assert_bits_equal(f"{tag} scale_v", sv[c:d], hsv)
             assert_bits_equal(f"{tag} v_min", vm[c:d], hvm)
-            assert_params_close(p[a:b], hp, p_prev)
+            assert_params_close(p[a:b], hp, p_prev, label=f"config 2 {tag}")
 
 
 def test_gpt2_small_set_through_the_optimizer():

@@ -19,6 +19,7 @@ import torch
 
 import mdq_hip
 from oracle import mdq_oracle as orc
+from param_bar import assert_param_bar
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -62,11 +63,7 @@ def check_against_oracle(snap, step, p, codes, sm, sv, vm):
         assert np.array_equal(host(codes[s:e]), hc), f"packed codes differ, {where}"
         for name, t, a in (("scale_m", sm, hsm), ("scale_v", sv, hsv), ("v_min", vm, hvm)):
             assert np.array_equal(host(t[b0:b1]).view(np.uint32), a.view(np.uint32)), f"{name} differs, {where}"
-        got = host(p[s:e]).astype(np.float64)
-        ref = hp.astype(np.float64)
-        err = np.abs(got - ref)
-        tol = 1e-6 * (np.abs(ref) + np.abs(ref - p_prev.astype(np.float64))) + 1e-30
-        assert np.all(err <= tol), f"params differ, {where}: max err {err.max():.3e}"
+        assert_param_bar(host(p[s:e]), hp, p_prev, label=f"2^31+ tensor, {where}")
 
 
 def test_tensor_beyond_2_31_elements():

@@ -68,4 +68,4 @@ def test_llama7b_set_three_steps_on_slices():
             assert_bits_equal(f"{tag} scale_m", sm[c:d], hsm)
             assert_bits_equal(f"{tag} scale_v", sv[c:d], hsv)
             assert_bits_equal(f"{tag} v_min", vm[c:d], hvm)
-            assert_params_close(p[a:b], hp, p_prev)
+            assert_params_close(p[a:b], hp, p_prev, label=f"config 4 {tag}")

@@ -1,9 +1,11 @@
 """GPU parity: the HIP kernels (through the C ABI) against the CPU oracle.
 
-Bar: packed codes, int codes and the three block-scale arrays bit-exact;
-params within 1e-6 relative (per element: |dp| <= 1e-6 * (|p| + |update|),
-and max|dp| <= 1e-6 * max|p|), because the device update uses the hardware
-sqrt/reciprocal while the oracle uses IEEE sqrtf and division.
+Bar: packed codes, int codes and the three block-scale arrays bit-exact; params per element
+within |dp| <= 2^-20 |update| + 2^-22 |p'| of the oracle's (the error bound of the device
+update, which uses the hardware sqrt / reciprocal where the oracle uses IEEE sqrtf and division;
+derived in tests/param_bar.py).  Every comparison records its per-element error distribution
+(share bit-identical, quantiles of |dp|/|p'|, the share above 1e-6 relative), which the session
+prints at its end.
 """
 import numpy as np
 import pytest
@@ -11,6 +13,7 @@ import torch
 
 import mdq_hip
 from oracle import mdq_oracle as orc
+from param_bar import assert_param_bar
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda:0")
@@ -38,18 +41,13 @@ def assert_bits_equal(name, t, a):
         raise AssertionError(f"{name}: {bad.size} mismatches, first at {bad[:5]} got {got[bad[:5]]} want {a[bad[:5]]}")
 
 
-def assert_params_close(p_gpu, p_ref, p_prev):
-    """One step from identical inputs: |dp| <= 1e-6 (|p| + |update|) per element."""
-    got = p_gpu.cpu().numpy().astype(np.float64)
-    ref = p_ref.astype(np.float64)
-    upd = np.abs(ref - p_prev.astype(np.float64))
-    err = np.abs(got - ref)
-    tol = 1e-6 * (np.abs(ref) + upd) + 1e-30
-    if not np.all(err <= tol):
-        i = int(np.argmax(err / tol))
-        raise AssertionError(f"param {i}: got {got[i]!r} want {ref[i]!r} prev {p_prev[i]!r} "
-                             f"err {err[i]:.3e} update {upd[i]:.3e} ({err[i] / max(upd[i], 1e-300):.2e} of it)")
-    assert err.max() <= 1e-6 * np.abs(ref).max()
+def assert_params_close(p_gpu, p_ref, p_prev, label=""):
+    """One step from identical inputs: |dp| <= 2^-20 |update| + 2^-22 |p'| per element (the
+    device update's error bound, tests/param_bar.py), and max|dp| <= 1e-6 max|p'|."""
+    got = p_gpu.cpu().numpy() if isinstance(p_gpu, torch.Tensor) else np.asarray(p_gpu)
+    assert_param_bar(got, p_ref, p_prev, label=label)
+    err = np.abs(got.astype(np.float64) - p_ref.astype(np.float64))
+    assert err.max() <= 1e-6 * np.abs(p_ref.astype(np.float64)).max()
 
 
 def resync_params(tp, p):
@@ -161,7 +159,7 @@ def test_config1_flat_4m_packed4_ten_steps():
         assert_bits_equal(f"step {step} scale_m", tsm, st[2])
         assert_bits_equal(f"step {step} scale_v", tsv, st[3])
         assert_bits_equal(f"step {step} v_min", tvm, st[4])
-        assert_params_close(tp, p, p_prev)
+        assert_params_close(tp, p, p_prev, label=f"config 1 step {step}")
         resync_params(tp, p)
 
 
