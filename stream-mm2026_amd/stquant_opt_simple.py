@@ -31,8 +31,13 @@ New optional param-group keys (the defaults keep the reference's behaviour):
 New constructor options:
 - ``sync_timing=False`` skips the device synchronisations that fill the timing dict and the
   kernel phase profile, so ``step()`` issues its work asynchronously on the current stream.
-- ``grad_stats='reference'`` computes the bit decision's statistics with the reference's per-tensor
-  torch reductions instead of the fused launch.
+- ``grad_stats`` chooses where the bit decision's statistics come from. ``'fused'`` (the default):
+  one fused launch for all tensors, exact to fp64; the tensors whose score lies within
+  ``SETTLE_MARGIN`` of a width threshold, and the near-constant ones (spread below
+  ``NEAR_CONSTANT_R`` of the mean magnitude, where the reference's fp32 ``torch.std`` loses digits),
+  are then scored on the reference's own torch reductions, so the widths are the reference's.
+  ``'reference'``: the reference's per-tensor torch reductions for every tensor.  ``'exact'``: the
+  fused statistics alone.
 """
 from __future__ import annotations
 
@@ -133,8 +138,8 @@ class MDQAdamWSimple(Optimizer):
         if bits is not None and int(bits) not in _REPORTED_WIDTHS:
             raise ValueError(f"bits must be one of 4, 8, 16, 32 or None, got {bits}")
         mdq_hip.rounding_code(rounding)
-        if grad_stats not in ("fused", "reference"):
-            raise ValueError(f"grad_stats must be 'fused' or 'reference', got {grad_stats!r}")
+        if grad_stats not in ("fused", "reference", "exact"):
+            raise ValueError(f"grad_stats must be 'fused', 'reference' or 'exact', got {grad_stats!r}")
         # the schedule's time constant, stquant_opt_simple.py:33
         tau = 300 * math.log(layer_count) * math.sqrt(batch_size)
         super().__init__(params, dict(lr=lr, betas=betas, eps=eps, weight_decay=weight_decay, alpha=alpha,
@@ -146,6 +151,7 @@ class MDQAdamWSimple(Optimizer):
         self.last_step_timings = {}
         self.sync_timing = sync_timing
         self.grad_stats = grad_stats
+        self._settled = 0                   # rows of the last decision taken from torch's reductions
         self._profile = _PhaseProfile()
 
     # launch-plan class of ``_run_kernels`` (a test harness substitutes its own executor)
@@ -176,25 +182,59 @@ class MDQAdamWSimple(Optimizer):
         v_l = torch.mean(grad * grad)
         return torch.stack([n_l, r_l, v_l])
 
-    def _all_grad_stats(self, grads):
-        """``[n, 3]`` stats of all grads: one fused launch per grad dtype, or the reference's
-        per-tensor torch reductions (``grad_stats="reference"``, stquant_opt_simple.py:427-431)."""
-        if self.grad_stats == "fused" and grads and grads[0].is_cuda:
-            return mdq_hip.grad_stats(grads)
+    # Scores this close to a width threshold, and tensors whose spread is below this fraction of
+    # their mean magnitude (r_l), take the reference's torch statistics in the default mode.  The
+    # fused statistics are exact to fp64; torch's fp32 reductions differ from them by less than
+    # 1e-4 in the score except for near-constant tensors, where torch.std loses digits (up to
+    # ~1e-2 in the score at r_l ~ 1e-5; tests/test_gpu_grad_stats.py).
+    SETTLE_MARGIN = 1e-2
+    NEAR_CONSTANT_R = 5e-2
+
+    def _all_grad_stats(self, grads, steps=None, tau=None):
+        """``[n, 3]`` stats of all grads: one fused launch per grad dtype (``'fused'``, settled on
+        the reference's torch reductions near the thresholds, and ``'exact'``), or the reference's
+        per-tensor torch reductions (``'reference'``, stquant_opt_simple.py:427-431)."""
+        if self.grad_stats != "reference" and grads and grads[0].is_cuda:
+            stats = mdq_hip.grad_stats(grads)
+            if self.grad_stats == "fused" and steps is not None:
+                stats = self._settle(stats, grads, steps, tau)
+            return stats
         return torch.stack([self._compute_grad_stats(g.float()) for g in grads])
 
-    def _scores(self, stats_tensor, steps, tau):
+    def _settle(self, stats, grads, steps, tau):
+        """The fused statistics, with the rows of the tensors whose width the fused and the
+        reference statistics could decide differently replaced by the reference's torch
+        reductions: scores within SETTLE_MARGIN of a threshold (provisional scores against the
+        EMAs this decision would fold in), near-constant tensors, and non-finite rows."""
+        prov = self._scores(stats, steps, tau, ema=self._folded_ema(stats.mean(dim=0)))
+        host = torch.cat((prov, stats[:, 1])).cpu().numpy()
+        sc, r = host[:len(grads)], host[len(grads):]
+        near = np.zeros(len(grads), dtype=bool)
+        for _bits, lo in _WIDTH_THRESHOLDS:
+            near |= np.abs(sc - lo) < self.SETTLE_MARGIN
+        redo = np.nonzero(near | (r < self.NEAR_CONSTANT_R) | ~np.isfinite(sc) | ~np.isfinite(r))[0].tolist()
+        if not redo:
+            return stats
+        stats = stats.clone()
+        stats[torch.as_tensor(redo, device=stats.device)] = torch.stack(
+            [self._compute_grad_stats(grads[i].float()) for i in redo])
+        self._settled = len(redo)
+        return stats
+
+    def _scores(self, stats_tensor, steps, tau, ema=None):
         """The reference's per-tensor score (stquant_opt_simple.py:446-466) for all tensors at
-        once: the same fp32 torch expressions, element for element, on ``[n]`` vectors."""
+        once: the same fp32 torch expressions, element for element, on ``[n]`` vectors.
+        ``ema``: (n, r, v) EMAs to score against instead of the optimizer's."""
+        n_ema, r_ema, v_ema = ema if ema is not None else (self.n_ema, self.r_ema, self.v_global_ema)
         n_l, r_l, v_l = stats_tensor[:, 0], stats_tensor[:, 1], stats_tensor[:, 2]
         t = torch.tensor([s / tau for s in steps], device=stats_tensor.device, dtype=torch.float32)
         s_t = 1.0 + (1.0 / torch.cosh(t))
         return (
             7.2
-            + torch.log2(r_l / (self.r_ema + 1e-12))
-            + torch.log2(n_l / (self.n_ema + 1e-12))
+            + torch.log2(r_l / (r_ema + 1e-12))
+            + torch.log2(n_l / (n_ema + 1e-12))
             + torch.log2(s_t)
-            + torch.log2(v_l / (self.v_global_ema + 1e-12))
+            + torch.log2(v_l / (v_ema + 1e-12))
         )
 
     @staticmethod
@@ -203,24 +243,31 @@ class MDQAdamWSimple(Optimizer):
         s = float(score.item()) if torch.is_tensor(score) and score.numel() == 1 else float(score)
         return next((bits for bits, lo in _WIDTH_THRESHOLDS if s >= lo), 4)
 
-    def _fold_ema(self, mean: torch.Tensor) -> None:
-        """Fold this decision's mean statistics ``[n, r, v]`` into the global EMAs (the first
-        decision assigns them); the same fp32 ops per component as the reference's :433-440."""
+    def _folded_ema(self, mean: torch.Tensor):
+        """The global EMAs ``(n, r, v)`` after folding in this decision's mean statistics
+        ``[n, r, v]`` (the first decision assigns them); the same fp32 ops per component as the
+        reference's :433-440."""
         if self.n_ema is None:
-            self.n_ema, self.r_ema, self.v_global_ema = mean.unbind(0)
-            return
+            return mean.unbind(0)
         a = self.param_groups[0]["alpha"]
         prev = torch.stack((self.n_ema, self.r_ema, self.v_global_ema))
-        self.n_ema, self.r_ema, self.v_global_ema = (a * mean + (1 - a) * prev).unbind(0)
+        return (a * mean + (1 - a) * prev).unbind(0)
+
+    def _fold_ema(self, mean: torch.Tensor) -> None:
+        self.n_ema, self.r_ema, self.v_global_ema = self._folded_ema(mean)
 
     def _decide_bits(self, work) -> None:
         """Score every tensor with a grad against the global statistics and give the tensors of
         scored groups their width; fills the decision's timing keys."""
         dev = work[0][0].device
         lt = self.last_step_timings
+        steps = [self.state[p]["step"] for p, _g in work]
+        tau = self.param_groups[0]["tau"]
+        self._settled = 0
         with _Stopwatch(dev) as sw:
-            stats = self._all_grad_stats([p.grad for p, _g in work])
+            stats = self._all_grad_stats([p.grad for p, _g in work], steps, tau)
         lt["mdq_grad_stats_ms"] = sw.ms
+        lt["mdq_grad_stats_settled"] = self._settled
         mean = stats.mean(dim=0)
         if dist.is_available() and dist.is_initialized():
             with _Stopwatch(dev) as sw:
@@ -230,7 +277,7 @@ class MDQAdamWSimple(Optimizer):
         with _Stopwatch(dev) as sw:
             self._fold_ema(mean)
             states = [self.state[p] for p, _g in work]
-            scores = self._scores(stats, [st["step"] for st in states], self.param_groups[0]["tau"])
+            scores = self._scores(stats, steps, tau)
             host = scores.cpu().tolist()                 # the step's one device -> host read
             for (_p, g), st, s, h in zip(work, states, scores.unbind(0), host):
                 st["last_score"] = s
@@ -626,8 +673,11 @@ class MDQAdamWSimple(Optimizer):
     def _make_steady(self, params_with_grad, runs):
         gpos = {id(g): k for k, g in enumerate(self.param_groups)}
         states = [self.state[p] for p, _g in params_with_grad]
+        with_grad = {id(p) for p, _g in params_with_grad}
+        every = [p for g in self.param_groups for p in g["params"]]
         return {
-            "ids": [id(p) for p, _g in params_with_grad],
+            "all_ids": [id(p) for p in every],
+            "nograd": [p for p in every if id(p) not in with_grad],
             "params": [p for p, _g in params_with_grad],
             "states": states,
             "state_obj": self.state,
@@ -639,12 +689,13 @@ class MDQAdamWSimple(Optimizer):
     def _steady_lookup(self, update_decision: bool):
         """The cached steady state if this step may reuse it, else None.
 
-        Reuse needs: the same param objects with grads in the same order, the
+        Reuse needs: the same param objects in the groups in the same order, the
         same ``state`` dict, the same per-group bits / block size / rounding /
         seed, and no bit decision this step (scored groups re-decide bits on
         update steps).  Storage is only replaced by steps that re-pack, by
         ``load_state_dict`` and by ``add_param_group``, which all drop the cache;
-        a param whose ``data`` moved is caught by ``_steady_step``.
+        a param whose ``data`` moved, or whose grad appeared or went away, is
+        caught by ``_steady_step``.
         """
         sc = self.__dict__.get("_steady")
         if sc is None or sc["state_obj"] is not self.state:
@@ -653,8 +704,7 @@ class MDQAdamWSimple(Optimizer):
             return None
         if sc["cfg"] != self._group_cfg():
             return None
-        cur = [id(p) for g in self.param_groups for p in g["params"] if p.grad is not None]
-        if cur != sc["ids"]:
+        if list(map(id, [p for g in self.param_groups for p in g["params"]])) != sc["all_ids"]:
             return None
         return sc
 
@@ -664,9 +714,15 @@ class MDQAdamWSimple(Optimizer):
         changed) if a param or grad no longer matches its plan."""
         params, states = sc["params"], sc["states"]
         t0 = time.perf_counter()
+        grads = [p.grad for p in params]
+        if any(p.grad is not None for p in sc["nograd"]):
+            return False
         for plan, idx, _gidx in sc["runs"]:
-            sel = [params[i] for i in idx]
-            if not plan.try_set_params(sel) or not plan.try_set_grads([p.grad for p in sel]):
+            if len(sc["runs"]) == 1:
+                ok = plan.try_refresh(params, grads)
+            else:
+                ok = plan.try_refresh([params[i] for i in idx], [grads[i] for i in idx])
+            if not ok:
                 return False
         steps = []
         for st in states:

@@ -5,9 +5,11 @@
   unaligned views; NaN where torch gives NaN (numel 0 and 1), NaN / inf where NaN / inf grads or
   overflowing fp32 sums make them, as torch's fp32 reductions on the GPU do;
 - the variance exact for tensors whose mean dwarfs their spread (closed form);
-- over 320 tensors (zero-mean heavy-tailed, nonzero-mean, near-constant, outliers; 54 of them
-  scaled to sit 3e-4 .. 3e-2 from the 6.8 / 12 / 24 thresholds) the fused statistics give the
-  widths the reference's torch expression gives, and so does the optimizer over six steps;
+- over 320 tensors (zero-mean heavy-tailed, nonzero-mean, near-constant, outliers; 72 of them,
+  18 near-constant, scaled to sit 3e-4 .. 3e-2 from the 6.8 / 12 / 24 thresholds) the default
+  decision statistics (fused, settled on torch's reductions near a threshold and for
+  near-constant tensors) give the widths the reference's torch expression gives, and so does the
+  optimizer over six steps;
 - deterministic (bit-identical on repeat), and within 1e-5 of the reference's fp32 torch
   reductions run on the same device;
 - ``MDQAdamWSimple._scores`` (one [n] vector) bit-identical to the reference's per-tensor
@@ -238,48 +240,69 @@ def _ref_stats(grads):
 
 
 def test_widths_match_the_reference_near_thresholds():
-    print("case: bit decision over 320 tensors, 54 near a threshold", flush=True)
+    """Over 320 tensors of four kinds, 72 of them scaled so that their reference score sits
+    3e-4 .. 3e-2 from a width threshold -- 18 of those near-constant (spread 1e-5 of the mean,
+    where torch's fp32 std loses digits) -- the default decision statistics give the widths of
+    the reference's torch reductions.  The fused statistics alone ('exact') differ from torch's
+    by < 1e-4 in the score for the other kinds and by up to ~1e-2 for the near-constant ones,
+    enough to flip a width there; the default settles those rows on torch's reductions."""
+    print("case: bit decision over 320 tensors, 72 near a threshold (18 near-constant)", flush=True)
     grads = _many_grads(11)
     params = [torch.nn.Parameter(torch.zeros(1, device=DEV))]
-    opt = MDQAdamWSimple(params, layer_count=12, batch_size=8)
+    # alpha = 0: folding a decision's mean statistics into the EMAs keeps the EMAs set below, so
+    # the placements below do not move the scores of the other tensors
+    opt = MDQAdamWSimple(params, layer_count=12, batch_size=8, alpha=0.0)
+    assert opt.grad_stats == "fused"
     ema = _ref_stats(grads).float().nanmedian(dim=0).values
     opt.n_ema, opt.r_ema, opt.v_global_ema = ema.unbind(0)
     tau = opt.param_groups[0]["tau"]
     steps = [1 + (7 * i) % 400 for i in range(len(grads))]
 
-    def ref_scores():
-        return opt._scores(_ref_stats(grads), steps, tau)
+    def scored(stats):
+        # as a decision step: fold the EMAs with these statistics' mean, then score against them
+        return opt._scores(stats, steps, tau, ema=opt._folded_ema(stats.mean(dim=0))).cpu().numpy()
 
-    # scale 54 tensors so that the reference scores sit at threshold + delta: n_l scales with
+    # scale 72 tensors so that the reference scores sit at threshold + delta: n_l scales with
     # the grads, v_l with their square, r_l not at all, so a factor k moves the score by 3 log2 k
     targets = [t + dl for t in (6.8, 12.0, 24.0) for dl in (-3e-2, -3e-3, -3e-4, 3e-4, 3e-3, 3e-2)]
-    picks = [i for i in range(len(grads)) if i % 4 != 2][:3 * len(targets):3]
-    for _ in range(3):
-        sc = ref_scores().cpu().numpy()
-        for i, tgt in zip(picks, targets):
+    picks = ([i for i in range(len(grads)) if i % 4 != 2][:3 * len(targets):3] +
+             [i for i in range(len(grads)) if i % 4 == 2][:2 * len(targets):2])
+    for _ in range(4):
+        sc = scored(_ref_stats(grads))
+        for i, tgt in zip(picks, targets + targets):
             grads[i] = grads[i] * float(2.0 ** ((tgt - sc[i]) / 3.0))
-    ref = ref_scores().cpu().numpy()
-    fused = opt._scores(mdq_hip.grad_stats(grads), steps, tau).cpu().numpy()
-    dist = min(abs(float(ref[i]) - t) for i in range(len(grads)) for t in (6.8, 12.0, 24.0))
-    print(f"max |score fused - score torch| = {np.nanmax(np.abs(fused - ref)):.2e}; closest reference score "
-          f"to a threshold: {dist:.2e}", flush=True)
-    for i, tgt in zip(picks, targets):
-        assert abs(ref[i] - tgt) < 1e-4, (i, ref[i], tgt)
+    ref = scored(_ref_stats(grads))
+    exact = scored(mdq_hip.grad_stats(grads))
+    settled_stats = opt._all_grad_stats(grads, steps, tau)
+    settled = scored(settled_stats)
+    # torch's fp32 std of a near-constant tensor does not scale exactly with it, so those land
+    # within ~1e-3 of their targets rather than 1e-4
+    for i, tgt in zip(picks, targets + targets):
+        assert abs(ref[i] - tgt) < (1e-4 if i % 4 != 2 else 5e-3), (i, ref[i], tgt)
+    nc_near = sum(min(abs(float(ref[i]) - t) for t in (6.8, 12.0, 24.0)) < 3e-3 for i in picks if i % 4 == 2)
+    assert nc_near >= 6, nc_near
     bits_ref = [opt._score_to_bits(float(x)) for x in ref]
-    bits_fused = [opt._score_to_bits(float(x)) for x in fused]
-    assert bits_fused == bits_ref
-    assert sorted(set(bits_ref)) == [4, 8, 16, 32]
-    # Scores agree to the fp32 rounding of the reductions, except for the near-constant tensors
-    # (kind 2, std 1e-5 of the mean): there torch's fp32 reductions lose digits of the std, while
-    # the fused two-pass fp64 statistics match the float64 oracle.
+    bits_exact = [opt._score_to_bits(float(x)) for x in exact]
+    bits_settled = [opt._score_to_bits(float(x)) for x in settled]
     other = [i for i in range(len(grads)) if i % 4 != 2]
     near_const = [i for i in range(len(grads)) if i % 4 == 2]
-    assert np.nanmax(np.abs(fused - ref)[other]) < 1e-4
+    gap_other = float(np.nanmax(np.abs(exact - ref)[other]))
+    gap_nc = float(np.nanmax(np.abs(exact - ref)[near_const]))
+    flips = [i for i in range(len(grads)) if bits_exact[i] != bits_ref[i]]
+    print(f"|score fused - score torch|: other kinds max {gap_other:.2e}, near-constant max {gap_nc:.2e}; "
+          f"widths from the fused statistics alone differ on {len(flips)} tensors "
+          f"({sum(i % 4 == 2 for i in flips)} near-constant; {nc_near} near-constant tensors within 3e-3 of a "
+          f"threshold); default settled {opt._settled} rows on torch's reductions and picks the reference's "
+          f"width for all {len(grads)}", flush=True)
+    assert bits_settled == bits_ref
+    assert sorted(set(bits_ref)) == [4, 8, 16, 32]
+    assert gap_other < 1e-4
+    assert gap_nc < MDQAdamWSimple.NEAR_CONSTANT_R   # bounded; settled rows cover it anyway
+    assert opt._settled < len(grads) // 2            # most rows keep the fused statistics
+    # the fused statistics match the float64 oracle on the near-constant tensors too
     st = mdq_hip.grad_stats([grads[i] for i in near_const]).cpu().numpy()
     for k, i in enumerate(near_const):
         np.testing.assert_allclose(st[k], orc.grad_stats(grads[i].cpu().numpy()), rtol=1e-6)
-    print(f"near-constant tensors: max |score fused - score torch| {np.nanmax(np.abs(fused - ref)[near_const]):.2e}"
-          f" (torch's fp32 std), the fused statistics within 1e-6 of the float64 oracle", flush=True)
 
 
 def test_optimizer_widths_match_reference_stats_many_tensors():
