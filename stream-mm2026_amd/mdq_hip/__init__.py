@@ -24,7 +24,8 @@ __all__ = [
     "TensorState", "MultiTensorPlan", "fused_step", "multi_tensor_step", "multi_tensor_restore",
     "RESTORE_BLOCK_SIZES", "grad_stats", "step_table_uploads", "convert_codes", "empty_codes", "storage_of",
     "block_aligned_ranges", "shard_states",
-    "device_math", "device_math_digests", "device_log_approx_error", "host_math", "host_round_half_away",
+    "device_math", "device_math_digests", "device_log_approx_error", "device_hw_ulp_error", "host_math",
+    "host_round_half_away",
     "host_div_code_range", "host_philox",
     "lib", "rounding_code", "storage",
 ]
@@ -160,6 +161,7 @@ class MultiTensorPlan:
         self._grad_dtype = self.entries[0].grad.dtype if self.entries else None
         self._dev_index = self.entries[0].p.get_device() if self.entries else -1
         self._numel = self.arr["numel"].tolist()
+        self._last_p = self.arr["p"].tolist()         # param pointers as Python ints (try_refresh)
 
     def set_steps(self, steps) -> None:
         self.arr["step"] = steps
@@ -203,6 +205,30 @@ class MultiTensorPlan:
                 return False
             ptrs.append(p.data_ptr())
         self.arr["p"] = ptrs
+        self._last_p = ptrs
+        return True
+
+    def try_refresh(self, params: Sequence[torch.Tensor], grads: Sequence[torch.Tensor]) -> bool:
+        """``try_set_params`` and ``try_set_grads`` in one pass, for a steady optimizer step: a
+        param whose data pointer is the one this plan last launched with is checked for its
+        size only (its dtype, device and layout came with that storage), a param at a new
+        address fully; a grad for its dtype and contiguity (torch ties a param's grad to the
+        param's size and device).  False (nothing changed) when something no longer fits."""
+        if len(params) != self.n or len(grads) != self.n:
+            return False
+        tdt, di, last = self._grad_dtype, self._dev_index, self._last_p
+        pp, gp = [], []
+        for k, (p, g, n) in enumerate(zip(params, grads, self._numel)):
+            a = p.data_ptr()
+            if a != last[k] and (p.dtype is not torch.float32 or p.get_device() != di or not p.is_contiguous()):
+                return False
+            if p.numel() != n or g is None or g.dtype is not tdt or not g.is_contiguous():
+                return False
+            pp.append(a)
+            gp.append(g.data_ptr())
+        self.arr["p"] = pp
+        self.arr["grad"] = gp
+        self._last_p = pp
         return True
 
     def set_hparams(self, lr=None, beta1=None, beta2=None, eps=None, weight_decay=None, bits=None) -> None:
@@ -439,6 +465,18 @@ def device_log_approx_error(first: int, count: int, slope: float = 0.0, device="
         check(lib().stq_device_log_approx_error(int(first), int(count), float(slope), out.data_ptr(),
                                                 _capi.stream_handle(dev)))
     return float(out.cpu().view(torch.float64).item())
+
+
+def device_hw_ulp_error(which: str, first: int, count: int, device="cuda:0") -> int:
+    """Largest ulp distance between the hardware sqrt (``which='sqrt'``) or reciprocal
+    (``'rcp'``) of the step's parameter update and the correctly rounded result, over the
+    floats with bit patterns first .. first+count-1."""
+    dev = torch.device(device)
+    out = torch.zeros(1, dtype=torch.int32, device=dev)
+    with torch.cuda.device(dev):
+        check(lib().stq_device_hw_ulp_error({"sqrt": 0, "rcp": 1}[which], int(first), int(count), out.data_ptr(),
+                                            _capi.stream_handle(dev)))
+    return int(out.cpu().item())
 
 
 def device_math(which: str, x: torch.Tensor) -> torch.Tensor:
