@@ -710,6 +710,7 @@ def profile_summary(args):
     with ``--copy-gib`` so the plain copy's counters calibrate them, and an SQ counter run."""
     shapes_fn, gdt, cfg_bits, B = CONFIGS[args.config]
     bits = cfg_bits if args.bits is None else args.bits
+    B = B if args.block is None else args.block
     N = sum(n for _, n in shapes_fn())
     if args.grad_stats:
         # the statistics kernel reads every grad once

@@ -178,6 +178,11 @@ template <> struct GradIO<GT_F32> {
 #pragma unroll
         for (int c = 0; c < 4; ++c) o[c] = q[c];
     }
+    // four grads from LDS at a 16-byte aligned address (one 16-byte read)
+    static __device__ __forceinline__ void lds4a(const char *a, float *o) {
+        const vf4 v = *(const vf4 *)a;
+        o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+    }
     static __device__ __forceinline__ void load4(const void *g, int64_t i, float *o) {
         vf4 v = ld_nt<vf4>(static_cast<const float *>(g) + i);
         o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
@@ -200,6 +205,8 @@ template <> struct GradIO<GT_BF16> {
 #pragma unroll
         for (int c = 0; c < 4; ++c) o[c] = bits_f((uint32_t)q[c] << 16);
     }
+    // four grads from LDS at an 8-byte aligned address (one 8-byte read)
+    static __device__ __forceinline__ void lds4a(const char *a, float *o) { unpack(*(const vu2 *)a, o); }
     static __device__ __forceinline__ void unpack(vu2 v, float *o) {
         o[0] = bits_f(v.x << 16); o[1] = bits_f(v.x & 0xffff0000u);
         o[2] = bits_f(v.y << 16); o[3] = bits_f(v.y & 0xffff0000u);
@@ -223,6 +230,8 @@ template <> struct GradIO<GT_F16> {
 #pragma unroll
         for (int c = 0; c < 4; ++c) o[c] = (float)__builtin_bit_cast(_Float16, q[c]);
     }
+    // four grads from LDS at an 8-byte aligned address (one 8-byte read)
+    static __device__ __forceinline__ void lds4a(const char *a, float *o) { unpack(*(const vu2 *)a, o); }
     static __device__ __forceinline__ float h2f(uint32_t h) {
         return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
     }
@@ -563,19 +572,28 @@ constexpr bool staged_mode()
 }
 
 // Bytes of LDS a one-wave staged tile uses for the lines of p (4 B per element) and
-// of the grads (GB B per element), each with one more line for a start inside a line.
-constexpr int staged_lds_bytes(int tile, int gb) { return 4 * tile + 128 + gb * tile + 128; }
+// of the grads (GB B per element), each with one more line for a start inside a line
+// and 16 bytes in front for the shifted base of lines_to_lds.
+constexpr int staged_lds_bytes(int tile, int gb) { return 16 + 4 * tile + 128 + 16 + gb * tile + 128; }
 
 // The 128-byte lines that hold src[0 .. NB) (bytes), as aligned 16-byte pieces from
-// the line of src's first byte on, into lds[0 ..) by direct global -> LDS loads
-// (non-temporal; piece w of the lines lands at lds + 16 w).  Lines are 128-byte
-// aligned, so none crosses a page: the bytes around src that they carry lie on
-// pages that src's own bytes map.  One wave; the caller waits (vmcnt) before
-// reading the LDS.
+// the line of src's first byte on, into LDS by direct global -> LDS loads
+// (non-temporal).  Piece w of the lines lands at lds - s + 16 w with s = off & 12 (the
+// direct loads write whole dwords, so the shift is a multiple of 4): src's byte b lands
+// at lds + (off & ~12) + b.  For a src on a 4-byte boundary (p, fp32 grads, 2-byte
+// grads at even element offsets) its 16-byte groups then start on 16-byte LDS
+// addresses (lds is 16-byte aligned with 16 bytes of room in front), and each lane
+// reads its quads as one aligned 16-byte (8-byte for 2-byte grads) LDS access.  With
+// the lines' own alignment instead, every quad of a view at an odd element offset
+// straddles 16-byte groups and takes element-wise reads, which the paired lane order
+// turns into 4-way bank conflicts.  Lines are 128-byte aligned, so none crosses a
+// page: the bytes around src that they carry lie on pages that src's own bytes map.
+// One wave; the caller waits (vmcnt) before reading the LDS.
 template <int NB>
 __device__ __forceinline__ void lines_to_lds(const void *src, char *lds, uint32_t off, int lane)
 {
     const char *l0 = (const char *)src - off;
+    lds -= off & 12u;
     const uint32_t nv = ((off + (uint32_t)NB + 127u) >> 7) * 8u;   // pieces of the covering lines
     constexpr int R = (NB / 16 + 8 + 63) / 64;
 #pragma unroll
@@ -648,8 +666,8 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
     static_assert(!STAGED || (C::QPL > 0 && C::WAVES == 1), "the staged mode is for one-wave tiles of quads");
     constexpr uint32_t GB = GT == GT_F32 ? 4u : 2u;       // bytes per grad
     // STAGED: pst holds the lines of p (later the staged p stores), then those of g
-    char *const stp = (char *)pst;
-    char *const stg = (char *)pst + 4 * C::TILE + 128;
+    char *const stp = (char *)pst + 16;
+    char *const stg = (char *)pst + 16 + 4 * C::TILE + 128 + 16;
     uint32_t offp = 0, offg = 0;                          // p's / g's byte offset in their first line
 
     unsigned long long t0 = 0;
@@ -779,10 +797,23 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
         }
     }
 
-    // exp table of the 16 packed v codes of this block (stquant_kernel.cu:75)
+    // exp table of the 16 packed v codes of this block (stquant_kernel.cu:75).  The
+    // arguments fma(e, sv, vmin), e = 0 .. 15, are non-decreasing in e when sv >= 0, so they
+    // lie in [vmin, fma(15, sv, vmin)]; when that interval is inside [-104, 89] for every
+    // block of the wave, mdq_expf_core gives mdq_expf's bits without its clamps and selects
+    // (as the per-element exp below).
     if constexpr (USE_LUT) {
         float *tab = lut + bi * 16;
-        if (blk_ok) {
+        const bool in = !blk_ok || (sv >= 0.0f && vmin >= -104.0f && fma_(15.0f, sv, vmin) <= 89.0f);
+        if (__builtin_amdgcn_ballot_w64(!in) == 0) {
+            if (blk_ok) {
+#pragma unroll
+                for (int r = 0; r < (16 + LPB - 1) / LPB; ++r) {
+                    const int e = j + r * LPB;
+                    if (e < 16) tab[e] = mdq_expf_core(fma_((float)e, sv, vmin));
+                }
+            }
+        } else if (blk_ok) {
 #pragma unroll
             for (int r = 0; r < (16 + LPB - 1) / LPB; ++r) {
                 const int e = j + r * LPB;
@@ -806,9 +837,13 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
 #pragma unroll
         for (int k = 0; k < C::QPL; ++k) {
             const uint32_t i = lbase + 4 * lane_quad<PAIRED, LOG2B>(j, k);
-            const float *q = (const float *)(stp + offp) + i;
-            pv[4 * k + 0] = q[0]; pv[4 * k + 1] = q[1]; pv[4 * k + 2] = q[2]; pv[4 * k + 3] = q[3];
-            GradIO<GT>::lds4(stg + offg + GB * i, gv + 4 * k);
+            // aligned quads: lines_to_lds shifted the lines by off & 12 (p is 4-byte aligned)
+            const vf4 q = *(const vf4 *)(stp + (offp & ~15u) + 4 * i);
+            pv[4 * k + 0] = q.x; pv[4 * k + 1] = q.y; pv[4 * k + 2] = q.z; pv[4 * k + 3] = q.w;
+            if (GB == 4 || (offg & 3u) == 0)
+                GradIO<GT>::lds4a(stg + (offg & ~15u) + GB * i, gv + 4 * k);
+            else   // 2-byte grads at an odd element offset: element-wise reads
+                GradIO<GT>::lds4(stg + (offg & ~12u) + GB * i, gv + 4 * k);
         }
     }
     if (prof_on) { unsigned long long t = clock64(); pa.c[0] += t - t0; t0 = t; }
@@ -979,7 +1014,10 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
                 inv_dm = 1.0f / dm;
                 inv_dv = 1.0f / dv;
             }
-            float um[EPL], uv[EPL];
+            // um: the m code's uniform; uvh: the v code's uniform minus 1/2 (exact: the
+            // centred 2^-16 grid minus 1/2 is a multiple of 2^-17 below 1/2), so that the fast
+            // path rounds to nearest where floor(z + uv) = rint(z + uvh) away from integers
+            float um[EPL], uvh[EPL];
             // Philox4x32 (MDQ_SR_ROUNDS rounds) per 4-element quad of the tensor:
             // counter (quad index lo, hi, tensor id, step), key = seed; word i of
             // the output serves element 4q+i (low half -> m, high half -> v).
@@ -989,7 +1027,7 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
 #pragma unroll
                 for (int e = 0; e < EPL; ++e) {
                     um[e] = mdq_u16_uniform(rw[e] & 0xffffu);
-                    uv[e] = mdq_u16_uniform(rw[e] >> 16);
+                    uvh[e] = mdq_u16_uniform_minus_half(rw[e] >> 16);
                 }
             } else {
 #pragma unroll
@@ -1001,16 +1039,19 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
                     const uint32_t w[4] = {r.x, r.y, r.z, r.w};
                     const uint32_t ww = w[idx & 3];
                     um[e] = mdq_u16_uniform(ww & 0xffffu);
-                    uv[e] = mdq_u16_uniform(ww >> 16);
+                    uvh[e] = mdq_u16_uniform_minus_half(ww >> 16);
                 }
             }
             if (fastv) {
                 // The exact code is floor(T), T = fl(fma(u, fl(1/dv), uv)), u = fl(log x - vmin).
-                // Z = fl(z + uv) with z = fl(log2_hw(x) * c1 + c0) as in the nearest path
-                // differs from T by at most G / dv + 5 (QV + 2) 2^-24 (G / dv: the nearest
-                // path's log and c1 / c0 term; the rest: the roundings of u, of z, of
-                // u / dv vs u * fl(1/dv), of T and of Z).  Where Z is farther than that from an
-                // integer, floor(Z) is the code; the other elements take the exact path.
+                // Zh = fl(z + uvh), z = fl(log2_hw(x) * c1 + c0) as in the nearest path and
+                // uvh = uv - 1/2 (exact), differs from T - 1/2 by at most G / dv + 5 (QV + 2) 2^-24
+                // (G / dv: the nearest path's log and c1 / c0 term; the rest: the roundings of
+                // u, of z, of u / dv vs u * fl(1/dv), of T and of Zh, which is no larger than
+                // |Zh| 2^-24 < (QV + 1) 2^-24).  Where Zh is farther than that from a
+                // half-integer, T - 1/2 lies within 1/2 of k = rint(Zh), so k < T < k + 1 and
+                // floor(T) = k: one rint and one test per element; the other elements take the
+                // exact path.
                 const VCodeMap vmap = mdq_vcode_map(dv, s_vmin);
                 const float r = vmap.r, c1 = vmap.c1, c0 = vmap.c0;
                 const float L = fmaxf(fabsf(lmax), fabsf(lmin));
@@ -1022,11 +1063,10 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
 #pragma unroll
                 for (int e = 0; e < EPL; ++e) {
                     qmf[e] = floor_(fma_(m[e], inv_dm, um[e]));
-                    const float Z = fma_(__builtin_amdgcn_logf(v[e] + 1e-12f), c1, c0) + uv[e];
-                    const float fz = floor_(Z);
-                    const float f = Z - fz;
-                    qvf[e] = fz;
-                    redo[e] = f <= ep || f >= 1.0f - ep;
+                    const float Zh = fma_(__builtin_amdgcn_logf(v[e] + 1e-12f), c1, c0) + uvh[e];
+                    const float k = rint_(Zh);
+                    qvf[e] = k;
+                    redo[e] = fabsf(Zh - k) >= 0.5f - ep;
                     any = any || redo[e];
                 }
                 if (__builtin_amdgcn_ballot_w64(any)) {
@@ -1034,7 +1074,8 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
 #pragma unroll
                     for (int e = 0; e < EPL; ++e) {
                         if (flat) qvf[e] = 0.0f;
-                        else if (redo[e]) qvf[e] = floor_(fma_(mdq_logf(v[e] + 1e-12f) - s_vmin, inv_dv, uv[e]));
+                        else if (redo[e])
+                            qvf[e] = floor_(fma_(mdq_logf(v[e] + 1e-12f) - s_vmin, inv_dv, uvh[e] + 0.5f));
                     }
                 }
             } else {
@@ -1044,7 +1085,7 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
                 for (int e = 0; e < EPL; ++e) {
                     const float u = lv[e] - s_vmin;
                     qmf[e] = sm_fin && fabsf(m[e]) <= __FLT_MAX__ ? floor_(fma_(m[e], inv_dm, um[e])) : 0.0f;
-                    qvf[e] = sv_fin && u <= __FLT_MAX__ ? floor_(fma_(u, inv_dv, uv[e])) : 0.0f;
+                    qvf[e] = sv_fin && u <= __FLT_MAX__ ? floor_(fma_(u, inv_dv, uvh[e] + 0.5f)) : 0.0f;
                 }
             }
         } else {

@@ -236,6 +236,13 @@ __device__ __forceinline__ U4 mdq_philox4x32_uk(U4 c, uint32_t k0, uint32_t k1)
 // (k16 + 0.5) / 2^16 as k16 * 2^-16 + 2^-17: both terms and the sum are exact
 // (17 significant bits), so the one fma equals the add-then-multiply form.
 MDQ_HD float mdq_u16_uniform(uint32_t k16) { return fma_((float)k16, 1.0f / 65536.0f, 1.0f / 131072.0f); }
+// The same uniform minus 1/2: (2 k16 + 1 - 65536) 2^-17, a multiple of 2^-17 of magnitude below
+// 1/2, so the fma (whose addend 2^-17 - 1/2 is exact too) is exact and
+// mdq_u16_uniform_minus_half(k) + 0.5f == mdq_u16_uniform(k) exactly.
+MDQ_HD float mdq_u16_uniform_minus_half(uint32_t k16)
+{
+    return fma_((float)k16, 1.0f / 65536.0f, 1.0f / 131072.0f - 0.5f);
+}
 
 // 1 / d correctly rounded for a positive normal d below 2^126 (where 1 / d is a
 // normal float).  On the device: the hardware reciprocal r (within 1 ulp) and

@@ -99,7 +99,9 @@ def test_config3_learnable_tokens_stochastic_vs_nearest_vs_adamw():
     than stochastic rounding: nearest rounds the many small m entries of a block to 0, and
     stochastic rounding keeps them in expectation.  Measured: stochastic ahead of nearest by up
     to 4 % at a step there.  The bars: the mean per-step gap between stochastic and nearest
-    within 1 %; final losses (last 50 steps) within 1 % of each other and of AdamW; and the
+    within 1 %; from step 100 on, where the loss still moves but no longer steeply (from about
+    5.60 down to 5.55), the stochastic curve within 1 % of the nearest one and of AdamW's at
+    every step; final losses (last 50 steps) within 1 % of each other and of AdamW; and the
     stochastic curve no farther from AdamW's (sum of losses) than the nearest one."""
     runs = {k: _run_full(n, r, vocab_used=256)
             for k, (n, r) in {"sr": ("MDQAdamW-Simple-FusedIO", "stochastic"),
@@ -109,14 +111,19 @@ def test_config3_learnable_tokens_stochastic_vs_nearest_vs_adamw():
     first = {k: float(v[0]) for k, v in loss.items()}
     final = {k: float(v[-50:].mean()) for k, v in loss.items()}
     rel = np.abs(loss["sr"] - loss["rn"]) / loss["rn"]
+    rel_adamw = np.abs(loss["sr"] - loss["adamw"]) / loss["adamw"]
+    late = slice(99, None)                               # steps 100 .. 300
     area = {k: abs(loss[k].sum() - loss["adamw"].sum()) / loss["adamw"].sum() for k in ("sr", "rn")}
     print(f"config 3 learnable: first {first} final (last 50) {final} (log 256 = {math.log(256):.3f}); "
           f"SR vs nearest per-step gap mean {rel.mean():.2e} max {rel.max():.2e} (step {int(rel.argmax()) + 1}); "
-          f"summed-loss gap to AdamW: SR {area['sr']:.2e}, nearest {area['rn']:.2e}", flush=True)
+          f"summed-loss gap to AdamW: SR {area['sr']:.2e}, nearest {area['rn']:.2e}; steps 100-300: SR vs nearest "
+          f"max {rel[late].max():.2e}, SR vs AdamW max {rel_adamw[late].max():.2e}, loss moving "
+          f"{loss['sr'][99]:.4f} -> {loss['sr'][-1]:.4f}", flush=True)
     for k in loss:
         assert first[k] > math.log(256) + 4.0 and final[k] < first[k] - 4.0, k
     assert len(set(first.values())) == 1                 # same init and data
     assert rel.mean() <= 0.01
+    assert rel[late].max() <= 0.01 and rel_adamw[late].max() <= 0.01
     assert abs(final["sr"] - final["rn"]) <= 0.01 * final["rn"]
     for k in ("sr", "rn"):
         assert abs(final[k] - final["adamw"]) <= 0.01 * final["adamw"], k

@@ -96,3 +96,19 @@ def test_new_v_scale_division_is_ieee(bits):
     got = mdq_hip.host_div_code_range(x, bits)
     assert np.array_equal(got.view(np.uint32), (x / D).astype(np.float32).view(np.uint32))
     assert np.isnan(mdq_hip.host_div_code_range(np.array([np.nan], np.float32), bits)[0])
+
+
+def test_centred_uniform_minus_half_is_exact():
+    """The stochastic v code's fast path rounds z + (u - 1/2) to nearest, with u on the centred
+    2^-16 grid (k + 1/2) / 65536 (the oracle's uniforms, mdq_oracle.c sr_uniforms): for every
+    16-bit k, k * 2^-16 + (2^-17 - 1/2) is exact in fp32 (its fma and its addend too), and adding
+    1/2 back gives the uniform itself exactly."""
+    k = np.arange(65536, dtype=np.float32)
+    c = np.float32(2.0 ** -17 - 0.5)
+    assert float(c) == 2.0 ** -17 - 0.5
+    exact = k.astype(np.float64) * 2.0 ** -16 + (2.0 ** -17 - 0.5)
+    uh = (k.astype(np.float64) * 2.0 ** -16 + float(c)).astype(np.float32)   # the fma, one rounding
+    assert np.array_equal(uh.astype(np.float64), exact)
+    u = (k * np.float32(2.0 ** -16) + np.float32(2.0 ** -17)).astype(np.float32)
+    assert np.array_equal(uh + np.float32(0.5), u)
+    assert np.all(np.abs(uh) < 0.5)
