@@ -523,6 +523,7 @@ def extra_configs(dev, steps: int, llama):
         log(f"{key}: {r['ms_per_step']:.4f} ms/step, kernel {r['kernel_ms']:.4f} ms, {100 * r['frac']:.1f} %")
         del w
         torch.cuda.empty_cache()
+    out["config2_gpt2_optimizer_step"] = optimizer_step_wall(dev, 100, 10)
     for key, views in (("config5", False), ("config5_views", True)):
         res = sweep_config5(dev, 20, 50, packed_views=views)
         out[key] = dict(params=res["params"], tensors=res["tensors"], grad_dtype="f32",
@@ -538,6 +539,42 @@ def extra_configs(dev, steps: int, llama):
     except ImportError as e:                      # transformers absent: the config cannot run here
         out["config3_gpt2_e2e"] = {"skipped": f"{type(e).__name__}: {e}"}
     return out
+
+
+def optimizer_step_wall(dev, steps: int, warmup: int):
+    """The drop-in optimizer's steady ``step()`` on the 148 GPT-2 small tensors (fp32 grads, 4-bit
+    state, B = 128, ``sync_timing=False``): wall ms per step over back-to-back steps, host path
+    included, beside the kernel's own time (HIP events around the same steps)."""
+    import torch
+
+    from stquant_opt_fused_io import MDQAdamWSimpleFusedIO
+
+    params = []
+    gen = torch.Generator(device=dev).manual_seed(3)
+    for _, n in gpt2_small_shapes():
+        prm = torch.nn.Parameter(torch.empty(n, device=dev).normal_(0.0, 0.02, generator=gen))
+        prm.grad = torch.empty(n, device=dev).normal_(0.0, 1e-3, generator=gen)
+        params.append(prm)
+    opt = MDQAdamWSimpleFusedIO(params, bits=4, block_size=128, sync_timing=False)
+    for _ in range(warmup):
+        opt.step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(steps):
+        opt.step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps * 1e3
+    r = dict(workload="MDQAdamWSimpleFusedIO.step() on the 148 GPT-2 small tensors, 4-bit, B=128, "
+                      "sync_timing=False, steady steps", steps=steps, warmup=warmup, ms_per_step=wall,
+             event_ms_per_step=ev0.elapsed_time(ev1) / steps, params=sum(p.numel() for p in params))
+    log(f"config 2 optimizer step(): {wall:.4f} ms wall per step ({r['event_ms_per_step']:.4f} ms by events)")
+    del opt, params
+    torch.cuda.empty_cache()
+    return r
 
 
 def e2e_share(steps: int, warmup: int):
