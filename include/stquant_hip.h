@@ -278,7 +278,10 @@ int stq_step_table_uploads(int64_t *count);
  * stq_device_math: y[i] = f(x[i]) for device arrays x, y of n floats; or, for
  *   which = 2 (n even), the step kernel's fast v-code map: for each pair
  *   (x[2i], x[2i+1]) = (dv, vmin), dv a positive normal float,
- *   (y[2i], y[2i+1]) = (ln 2 / dv, -vmin / dv) as the kernel computes them.
+ *   (y[2i], y[2i+1]) = (ln 2 / dv, -vmin / dv) as the kernel computes them;
+ *   for which = 4 (n a multiple of 6), the stochastic requant's fast v code:
+ *   for each 6-tuple (x, kv, dv, vmin, lmax, QV) the estimate Zh of T - 1/2 and
+ *   its error bound ep, as (Zh, ep, 0, 0, 0, 0).
  * stq_device_math_digests: for the bit patterns first .. first+count-1, the
  *   sum over each chunk of mix64(bits(x) << 32 | bits(f(x))) into
  *   digests[ceil(count / chunk)] (device uint64, zeroed by the caller).

@@ -167,6 +167,8 @@ int make_desc(const stq_tensor &t, int storage, int grad_dt, int B, MdqDesc &d)
     d.inv_qm = ldexpf(1.0f, -(t.bits - 1));
     d.qvf = (float)(std::ldexp(1.0, t.bits) - 1.0);
     d.inv_qvf = 1.0f / d.qvf;
+    d.ep0_rn = mdq::mdq_rn_ep0(d.qvf);
+    d.ep0_sr = mdq::mdq_sr_ep0(d.qvf);
     d.bits = (uint32_t)t.bits;
     d.step = (uint32_t)t.step;
     d.tensor_id = t.tensor_id;
@@ -902,9 +904,11 @@ int stq_step_table_uploads(int64_t *count)
 int stq_device_math(int which, const float *x, float *y, int64_t n, void *stream)
 {
     g_err.clear();
-    if (which < 0 || which > 3)
-        return fail(STQ_ERR_INVALID, "which must be 0 (exp), 1 (log), 2 (v-code map) or 3 (reciprocal)");
-    if (n < 0 || (n > 0 && (!x || !y)) || (which == 2 && n % 2)) return fail(STQ_ERR_INVALID, "bad arrays");
+    if (which < 0 || which > 4)
+        return fail(STQ_ERR_INVALID,
+                    "which must be 0 (exp), 1 (log), 2 (v-code map), 3 (reciprocal) or 4 (stochastic fast v code)");
+    if (n < 0 || (n > 0 && (!x || !y)) || (which == 2 && n % 2) || (which == 4 && n % 6))
+        return fail(STQ_ERR_INVALID, "bad arrays");
     hipError_t e = mdq::launch_math(which, x, y, n, reinterpret_cast<hipStream_t>(stream));
     return e == hipSuccess ? STQ_OK : hip_fail(e, "math kernel launch");
 }

@@ -49,9 +49,12 @@ struct alignas(16) MdqDesc {
     // Index of element 0 in the tensor's stochastic-rounding stream (a
     // multiple of B; nonzero for a piece of a larger tensor).
     int64_t rng_origin;
+    // The rounding terms of the fast v-code paths' error bounds for this width
+    // (mdq_rn_ep0 / mdq_sr_ep0 of qvf).
+    float ep0_rn, ep0_sr;
 };
 
-static_assert(sizeof(MdqDesc) % 16 == 0, "descriptor must stay 16-byte sized");
+static_assert(sizeof(MdqDesc) == 176, "descriptor layout: 176 bytes, 16-byte sized");
 
 // Kernel arguments of a step launch besides its table: the stochastic-rounding
 // key and, when every tensor of the launch has the same step_size,

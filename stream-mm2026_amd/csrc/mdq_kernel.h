@@ -47,6 +47,46 @@ namespace mdq {
 // Relative error bound of the fast v-code path's c1 + that of its c0 (each
 // within 2^-24 (1 + 2^-16) of the exact quotient; mdq_vcode_map).
 #define MDQ_VCODE_MAP_ERR 1.3e-7f
+// The stochastic v code's fast path.  The exact code is floor(T), T = fl(fma(u, fl(1/dv), uv)),
+// u = fl(log x - vmin), uv = (k + 1/2) 2^-16 with k the element's 16-bit random half.  The path
+// evaluates Zh = fl(z + uvh), z = fl(log2_hw(x) c1 + c0) with c1, c0 from mdq_vcode_map (as the
+// nearest path) and uvh = uv - 1/2 (exact: mdq_u16_uniform_minus_half), so that Zh approximates
+// T - 1/2.  |Zh - (T - 1/2)| <= ep, the sum of
+// - the hardware log and the quotients c1, c0 (the nearest path's term): (A + (S + 1.3e-7) L) / dv,
+//   L = max(|lmax|, |lmin|) >= |log x| and >= |vmin| in the block;
+// - the roundings of u, of z, of u / dv vs u fl(1/dv), of T and of Zh (|z|, |Zh| < QV + 1):
+//   5 (QV + 2) 2^-24 < 3e-7 (QV + 2),
+// with r = v_rcp_f32(dv) for 1 / dv (the factor 1.001 covers the difference; the last term is
+// the descriptor's ep0_sr, mdq_sr_ep0).  Where Zh lies farther than ep from a half-integer,
+// T - 1/2 lies within 1/2 of k = rint(Zh), so k < T < k + 1 and floor(T) = k.  Checked against
+// fp64 on the device (stq_device_math, which 4).
+struct SrVFast {
+    float c1, c0, ep;
+};
+// max(|lmax|, |vmin|) for vmin <= lmax, both finite: max(lmax, -vmin), one instruction (written
+// out: the compiler's maxnum first quiets both operands, two more instructions)
+__device__ __forceinline__ float mdq_log_span(float lmax, float vmin)
+{
+#if defined(__HIP_DEVICE_COMPILE__)
+    float r;
+    __asm__("v_max_f32_e64 %0, %1, -%2" : "=v"(r) : "v"(lmax), "v"(vmin));
+    return r;
+#else
+    return lmax > -vmin ? lmax : -vmin;
+#endif
+}
+__device__ __forceinline__ SrVFast mdq_sr_vfast(float dv, float vmin, float lmax, float ep0_sr)
+{
+    const VCodeMap vm = mdq_vcode_map(dv, vmin);
+    const float L = mdq_log_span(lmax, vmin);
+    const float ep = fma_(fma_(L, MDQ_LOG_APPROX_SLOPE + MDQ_VCODE_MAP_ERR, MDQ_LOG_APPROX_ERR), vm.r * 1.001f, ep0_sr);
+    return {vm.c1, vm.c0, ep};
+}
+// Zh for x = v + 1e-12 and the element's uvh = uv - 1/2 (see mdq_sr_vfast).
+__device__ __forceinline__ float mdq_sr_vfast_z(float x, float uvh, const SrVFast &f)
+{
+    return fma_(__builtin_amdgcn_logf(x), f.c1, f.c0) + uvh;
+}
 
 // Lanes per block of the paired code layout (paired_codes).
 constexpr bool paired_lpb(int lpb) { return lpb == 8 || lpb == 16 || lpb == 32; }
@@ -1043,38 +1083,32 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
                 }
             }
             if (fastv) {
-                // The exact code is floor(T), T = fl(fma(u, fl(1/dv), uv)), u = fl(log x - vmin).
-                // Zh = fl(z + uvh), z = fl(log2_hw(x) * c1 + c0) as in the nearest path and
-                // uvh = uv - 1/2 (exact), differs from T - 1/2 by at most G / dv + 5 (QV + 2) 2^-24
-                // (G / dv: the nearest path's log and c1 / c0 term; the rest: the roundings of
-                // u, of z, of u / dv vs u * fl(1/dv), of T and of Zh, which is no larger than
-                // |Zh| 2^-24 < (QV + 1) 2^-24).  Where Zh is farther than that from a
-                // half-integer, T - 1/2 lies within 1/2 of k = rint(Zh), so k < T < k + 1 and
-                // floor(T) = k: one rint and one test per element; the other elements take the
-                // exact path.
-                const VCodeMap vmap = mdq_vcode_map(dv, s_vmin);
-                const float r = vmap.r, c1 = vmap.c1, c0 = vmap.c0;
-                const float L = fmaxf(fabsf(lmax), fabsf(lmin));
-                const float ep = (fma_(L, MDQ_LOG_APPROX_SLOPE + MDQ_VCODE_MAP_ERR, MDQ_LOG_APPROX_ERR) * r +
-                                  fma_(d.qvf + 2.0f, 3.0e-7f, 0.0f)) *
-                                 1.001f;
+                // Zh approximates T - 1/2 within ep (mdq_sr_vfast): where Zh lies farther than
+                // ep from a half-integer, rint(Zh) is the exact code (one rint and one test per
+                // element); the elements of a wave with any closer Zh take the exact path.  In a
+                // flat block every x is equal, so log x - vmin = 0 and the code is floor(uv) = 0;
+                // there (its tiny dv flags every element) c1 = c0 = 0 make Zh = uvh exactly,
+                // |uvh| < 1/2, so rint(Zh) = 0 without the exact path.
+                const bool flat = kx == kn;
+                SrVFast f = mdq_sr_vfast(dv, s_vmin, lmax, d.ep0_sr);
+                f.c1 = flat ? 0.0f : f.c1;
+                f.c0 = flat ? 0.0f : f.c0;
+                const float near = 0.5f - f.ep;
                 bool redo[EPL];
                 bool any = false;
 #pragma unroll
                 for (int e = 0; e < EPL; ++e) {
                     qmf[e] = floor_(fma_(m[e], inv_dm, um[e]));
-                    const float Zh = fma_(__builtin_amdgcn_logf(v[e] + 1e-12f), c1, c0) + uvh[e];
+                    const float Zh = mdq_sr_vfast_z(v[e] + 1e-12f, uvh[e], f);
                     const float k = rint_(Zh);
                     qvf[e] = k;
-                    redo[e] = fabsf(Zh - k) >= 0.5f - ep;
+                    redo[e] = fabsf(Zh - k) >= near;
                     any = any || redo[e];
                 }
-                if (__builtin_amdgcn_ballot_w64(any)) {
-                    const bool flat = kx == kn;          // code floor(0 + uv) = 0
+                if (__builtin_amdgcn_ballot_w64(any && !flat)) {
 #pragma unroll
                     for (int e = 0; e < EPL; ++e) {
-                        if (flat) qvf[e] = 0.0f;
-                        else if (redo[e])
+                        if (redo[e] && !flat)
                             qvf[e] = floor_(fma_(mdq_logf(v[e] + 1e-12f) - s_vmin, inv_dv, uvh[e] + 0.5f));
                     }
                 }
@@ -1119,10 +1153,10 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
                 // faster than the exact rounding for every element; 4-bit level.
                 const VCodeMap vmap = mdq_vcode_map(dv, s_vmin);
                 const float r = vmap.r, c1 = vmap.c1, c0 = vmap.c0;
-                const float L = fmaxf(fabsf(lmax), fabsf(lmin));
-                const float ep = (fma_(L, MDQ_LOG_APPROX_SLOPE + MDQ_VCODE_MAP_ERR, MDQ_LOG_APPROX_ERR) * r +
-                                  fma_(d.qvf + 1.0f, 1.2e-7f, 0.0f)) *
-                                 1.001f;
+                const float L = mdq_log_span(lmax, s_vmin);
+                // the last term: the descriptor's ep0_rn = (QV + 1) 1.2e-7 * 1.001 (mdq_rn_ep0)
+                const float ep = fma_(fma_(L, MDQ_LOG_APPROX_SLOPE + MDQ_VCODE_MAP_ERR, MDQ_LOG_APPROX_ERR),
+                                      r * 1.001f, d.ep0_rn);
                 const float near = 0.5f - ep;
                 const float rdm = __builtin_amdgcn_rcpf(dm);
                 const float nearm = bigm ? -1.0f : 0.5f - fma_(d.qm, 6.0e-7f, 6.0e-7f);

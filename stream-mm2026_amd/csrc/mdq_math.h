@@ -232,6 +232,13 @@ __device__ __forceinline__ U4 mdq_philox4x32_uk(U4 c, uint32_t k0, uint32_t k1)
 }
 #endif
 
+// The rounding terms of the fast v-code paths' error bounds for codes in [0, qvf]
+// (qvf = 2^bits - 1), each with headroom and times the paths' factor 1.001 for
+// v_rcp_f32(dv) against 1 / dv: the nearest path's 2 (QV + 1) 2^-24 and the stochastic
+// path's 5 (QV + 2) 2^-24 (mdq_kernel.h, mdq_sr_vfast).  Per tensor, in its descriptor.
+MDQ_HD float mdq_rn_ep0(float qvf) { return (qvf + 1.0f) * 1.2e-7f * 1.001f; }
+MDQ_HD float mdq_sr_ep0(float qvf) { return (qvf + 2.0f) * 3.0e-7f * 1.001f; }
+
 // Uniforms on the centred 2^-16 grid: (k + 1/2) / 65536, k in [0, 65535].
 // (k16 + 0.5) / 2^16 as k16 * 2^-16 + 2^-17: both terms and the sum are exact
 // (17 significant bits), so the one fma equals the add-then-multiply form.

@@ -2,6 +2,7 @@
 // compared bit for bit with a CPU implementation.
 #include <hip/hip_runtime.h>
 
+#include "mdq_kernel.h"
 #include "mdq_launch.h"
 #include "mdq_math.h"
 
@@ -22,6 +23,17 @@ __global__ __launch_bounds__(256) void math_kernel(int which, const float *__res
             const VCodeMap m = mdq_vcode_map(x[2 * i], x[2 * i + 1]);
             y[2 * i] = m.c1;
             y[2 * i + 1] = m.c0;
+        }
+        return;
+    }
+    if (which == 4) {   // (x, kv, dv, vmin, lmax, QV) -> (Zh, ep, 0, 0, 0, 0) of the stochastic fast v code
+        for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n / 6;
+             i += (long long)gridDim.x * blockDim.x) {
+            const float *a = x + 6 * i;
+            const SrVFast f = mdq_sr_vfast(a[2], a[3], a[4], mdq_sr_ep0(a[5]));
+            y[6 * i] = mdq_sr_vfast_z(a[0], mdq_u16_uniform_minus_half((uint32_t)a[1]), f);
+            y[6 * i + 1] = f.ep;
+            for (int k = 2; k < 6; ++k) y[6 * i + k] = 0.0f;
         }
         return;
     }

@@ -482,10 +482,12 @@ def device_hw_ulp_error(which: str, first: int, count: int, device="cuda:0") -> 
 def device_math(which: str, x: torch.Tensor) -> torch.Tensor:
     """Device e^x (``which='exp'``), log x (``'log'``) or the stochastic requant's reciprocal
     (``'rcp'``) with the kernels' own fp32 code; or ``'vcode_map'``: x holds (dv, vmin) pairs,
-    the result the fast v-code path's (ln 2 / dv, -vmin / dv) pairs."""
+    the result the fast v-code path's (ln 2 / dv, -vmin / dv) pairs; or ``'sr_vfast'``: x holds
+    (x, kv, dv, vmin, lmax, QV) 6-tuples, the result (Zh, ep, 0, 0, 0, 0): the stochastic fast
+    v-code path's estimate of T - 1/2 and its error bound."""
     assert x.is_cuda and x.dtype == torch.float32 and x.is_contiguous()
     y = torch.empty_like(x)
-    code = {"exp": 0, "log": 1, "vcode_map": 2, "rcp": 3}[which]
+    code = {"exp": 0, "log": 1, "vcode_map": 2, "rcp": 3, "sr_vfast": 4}[which]
     with torch.cuda.device(x.device):
         check(lib().stq_device_math(code, _ptr(x), _ptr(y), x.numel(), _capi.stream_handle(x.device)))
     return y

@@ -108,3 +108,44 @@ def test_hardware_sqrt_and_reciprocal_within_one_ulp(which, first, count):
     ulps = mdq_hip.device_hw_ulp_error(which, first, count)
     print(f"{which}: max {ulps} ulp from the correctly rounded result over {count:,} floats", flush=True)
     assert ulps <= 1
+
+
+def test_stochastic_fast_vcode_bound():
+    """The stochastic requant's fast v-code path (mdq_sr_vfast, as the step kernel runs it) against
+    the exact code's T = fl(fma(u, fl(1/dv), uv)), u = fl(log x - vmin), uv = (k + 1/2) 2^-16 (the
+    oracle's definition, mdq_oracle.c): |Zh - (T - 1/2)| <= ep for blocks of 4- and 8-bit codes with
+    log spans from 1e-5 to 40 over the logs of [1e-12, FLT_MAX], and rint(Zh) = floor(T) wherever
+    Zh lies farther than ep from a half-integer.  A dropped term of the bound (or a wrong offset in
+    c0h) shows as a bound overrun or a code mismatch here."""
+    rng = np.random.default_rng(11)
+    n = 1 << 20
+    qv = np.where(rng.random(n) < 0.5, 15.0, 255.0).astype(np.float32)
+    lmin = rng.uniform(-27.6, 85.0, n).astype(np.float32)
+    span = (10.0 ** rng.uniform(-5, 1.6, n)).astype(np.float32)
+    lmax = np.minimum(lmin + span, np.float32(88.7)).astype(np.float32)
+    lsam = (lmin + (lmax - lmin) * rng.random(n)).astype(np.float64)
+    x = np.exp(lsam).astype(np.float32)
+    ok = np.isfinite(x) & (x >= np.float32(1e-12))
+    x, qv, lmin, lmax = x[ok], qv[ok], lmin[ok], lmax[ok]
+    l = orc.logf(x)                                          # the oracle's log of x
+    vmin = np.minimum(lmin, l).astype(np.float32)
+    lmax = np.maximum(lmax, l).astype(np.float32)
+    dv = ((lmax - vmin + np.float32(1e-12)) / qv + np.float32(1e-12)).astype(np.float32)
+    kv = rng.integers(0, 65536, x.size).astype(np.float32)
+    tup = np.stack([x, kv, dv, vmin, lmax, qv], 1).astype(np.float32).reshape(-1)
+    y = mdq_hip.device_math("sr_vfast", torch.from_numpy(tup).cuda()).cpu().numpy().reshape(-1, 6)
+    zh, ep = y[:, 0].astype(np.float64), y[:, 1].astype(np.float64)
+    u = (l - vmin).astype(np.float32)
+    inv = (np.float32(1.0) / dv).astype(np.float32)
+    uv = ((kv + np.float32(0.5)) * np.float32(1.0 / 65536.0)).astype(np.float32)
+    t = (u.astype(np.float64) * inv.astype(np.float64) + uv.astype(np.float64)).astype(np.float32)
+    err = np.abs(zh - (t.astype(np.float64) - 0.5))
+    assert np.all(err <= ep), (err / ep).max()
+    k = np.rint(zh)
+    fast = np.abs(zh - k) < 0.5 - ep
+    assert np.array_equal(k[fast], np.floor(t.astype(np.float64))[fast])
+    small = ep < 1e-3                 # typical blocks: the fast path decides nearly every code
+    print(f"sr fast v code: {x.size} samples, max err / ep {(err / ep).max():.3f}, fast-path share "
+          f"{fast.mean():.5f} ({fast[small].mean():.5f} where ep < 1e-3, {small.mean():.3f} of samples)",
+          flush=True)
+    assert small.mean() > 0.25 and fast[small].mean() > 0.99
