@@ -312,13 +312,18 @@ template <> struct CodeIO<ST_P4> {
         mc = (float)(b & 15u);
         vc = b >> 4;
     }
+    // The paired layout's codes in two steps: raw8 issues the lane's 8-byte load, decode8
+    // (after every load of the tile is in flight) swaps half of it with the pair lane.
     // vc receives 4 x the v code: the byte offset of its entry in the block's exp table.
     // Both nibble fields are masked once per word (the empty asm keeps the masks from being
     // folded into per-element bit-field extracts), so each element takes one byte-select
     // conversion (m) and one byte-select add (the table address).
+    typedef vu2 Raw8;
+    static __device__ __forceinline__ Raw8 raw8(const MdqDesc &d, uint32_t blk_off, int j) {
+        return ld_nt<vu2>(static_cast<const uint8_t *>(d.code_m) + blk_off + 8 * j);
+    }
     template <int H>
-    static __device__ __forceinline__ void load8(const MdqDesc &d, uint32_t blk_off, int j, float *mc, uint32_t *vc) {
-        const vu2 w = ld_nt<vu2>(static_cast<const uint8_t *>(d.code_m) + blk_off + 8 * j);
+    static __device__ __forceinline__ void decode8(Raw8 w, int j, float *mc, uint32_t *vc) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const uint32_t q = pair_in<H>(w, j, h);
@@ -381,10 +386,16 @@ template <> struct CodeIO<ST_S8> {
         mc = (float)ld_g<int8_t>(static_cast<const int8_t *>(d.code_m) + i);
         vc = ld_g<uint8_t>(static_cast<const uint8_t *>(d.code_v) + i);
     }
-    template <int H>
-    static __device__ __forceinline__ void load8(const MdqDesc &d, uint32_t blk_off, int j, float *mc, uint32_t *vc) {
+    // the paired layout's m and v codes: raw8 loads, decode8 swaps and converts (CodeIO<ST_P4>)
+    typedef vu4 Raw8;
+    static __device__ __forceinline__ Raw8 raw8(const MdqDesc &d, uint32_t blk_off, int j) {
         const vu2 wm = ld_nt<vu2>(static_cast<const int8_t *>(d.code_m) + blk_off + 8 * j);
         const vu2 wv = ld_nt<vu2>(static_cast<const uint8_t *>(d.code_v) + blk_off + 8 * j);
+        return vu4{wm.x, wm.y, wv.x, wv.y};
+    }
+    template <int H>
+    static __device__ __forceinline__ void decode8(Raw8 w, int j, float *mc, uint32_t *vc) {
+        const vu2 wm = {w.x, w.y}, wv = {w.z, w.w};
         const uint32_t m0 = pair_in<H>(wm, j, 0), m1 = pair_in<H>(wm, j, 1);
         const uint32_t v0 = pair_in<H>(wv, j, 0), v1 = pair_in<H>(wv, j, 1);
 #pragma unroll
@@ -473,6 +484,11 @@ template <> struct CodeIO<ST_S32> {
         st_g<uint32_t>(qv, static_cast<uint32_t *>(d.code_v) + i);
     }
 };
+
+// The raw words of CodeIO<ST>::raw8 (storages without the paired layout: unused).
+template <int ST> struct Raw8Of { typedef int type; };
+template <> struct Raw8Of<ST_P4> { typedef CodeIO<ST_P4>::Raw8 type; };
+template <> struct Raw8Of<ST_S8> { typedef CodeIO<ST_S8>::Raw8 type; };
 
 // ------------------------------------------------------- cross-lane reduction
 // Block reductions run on integer keys: |m| >= 0 orders like its bit pattern,
@@ -593,22 +609,25 @@ __device__ __forceinline__ float dequant_m(float code, float sm, float neg8sm)
 // LDS line by line (store_p_lines); codes move as in TILE_VECTOR.  Config 5 as
 // views back to back, B = 64: 64 % of HBM peak with the lanes' own element-aligned
 // vectors, 80 % staged, level with separate allocations.  TILE_UNALIGNED_PG (tiles
-// of more than one wave, and stochastic rounding from B = 128 on, staged_mode):
+// of more than one wave, and wider codes with stochastic rounding from B = 256 on,
+// staged_mode):
 // codes as in TILE_VECTOR, p and grads loaded as the lanes' vectors at element-aligned
 // addresses, and p stored through LDS when it does not start on a line.
 // TILE_GUARDED: every access element by element, guarded by idx < numel.
 enum TileMode : int { TILE_GUARDED = 0, TILE_VECTOR = 1, TILE_UNALIGNED_PG = 2, TILE_STAGED = 3 };
 
 // Whether tiles with p or grads off their 128-byte lines take TILE_STAGED (else
-// TILE_UNALIGNED_PG).  Same-box A/B on config 5 as packed views, stochastic rounding:
-// staging is faster up to B = 64 (B = 64 8-bit 71.6 -> 75.4 % of HBM peak, B = 32 4-bit
-// 66.0 -> 70.9 %), where each block's span of lanes covers at most one line, and slower
-// from B = 128 on (B = 256 4-bit 79.0 -> 74.0 %), where the Philox work leaves less room
-// for the LDS round trip.  Nearest rounding: faster at every B.
-template <bool SR, int LOG2B>
+// TILE_UNALIGNED_PG).  Same-allocation A/B on config 5 as packed views, stochastic
+// rounding, with the tile's loads all in flight before its first cross-lane DS
+// instruction (mdq_step_tile): staged against element-aligned vectors, B = 128 4-bit
+// 72.4 -> 78.7 % of HBM peak, 8-bit 74.2 -> 77.8 %; packed 4-bit codes B = 256 77.5 ->
+// 79.2 %, B = 512 78.6 -> 79.6 %; int8 + uint8 codes B = 256 level, B = 512 79.3 -> 78.5 %.
+// Nearest rounding: faster at every B.
+template <int SRC, int DST, bool SR, int LOG2B>
 constexpr bool staged_mode()
 {
-    return Cfg<LOG2B>::QPL > 0 && Cfg<LOG2B>::WAVES == 1 && (!SR || LOG2B <= 6);
+    return Cfg<LOG2B>::QPL > 0 && Cfg<LOG2B>::WAVES == 1 &&
+           (!SR || LOG2B <= 7 || (SRC == ST_P4 && DST == ST_P4));
 }
 
 // Bytes of LDS a one-wave staged tile uses for the lines of p (4 B per element) and
@@ -728,7 +747,11 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
     // old block scales (stquant_kernel.cu:67-69): the block's first lane of
     // each wave loads them and the block's other lanes take them by broadcast
     // (one active lane per block keeps the small loads from occupying the
-    // whole wave's address path).
+    // whole wave's address path).  The broadcasts, like the paired codes' lane
+    // swaps, are cross-lane DS instructions, and the compiler makes every DS
+    // instruction after a direct global -> LDS load (TILE_STAGED) wait for all
+    // loads in flight: they run after every load of the tile is issued and the
+    // Philox words are drawn, so the tile makes one memory round trip.
     float sm = 0.0f, sv = 0.0f, vmin = 0.0f;
     const bool loader = (LPB <= 64 ? j == 0 : lane == 0) && blk_ok;
     if (loader) {
@@ -736,13 +759,11 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
         sv = ld_g<float>(d.scale_v + blk);
         vmin = ld_g<float>(d.v_min + blk);
     }
-    sm = block_bcast<LPB>(sm);
-    sv = block_bcast<LPB>(sv);
-    vmin = block_bcast<LPB>(vmin);
 
     float pv[EPL], gv[EPL], mc[EPL];
     uint32_t vc[EPL];
     bool ok[EPL];
+    [[maybe_unused]] typename Raw8Of<SRC>::type craw{};   // paired 1-byte codes as loaded
     // FULL tiles address through a workgroup-uniform tile base (scalar
     // registers) plus a 32-bit lane offset, so loads and stores take the
     // saddr + voffset form instead of 64-bit per-lane address arithmetic.
@@ -772,7 +793,7 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
             }
             if constexpr (!(PAIRED && one_byte_codes(SRC))) CodeIO<SRC>::load4(dt, i, mc + 4 * k, vc + 4 * k);
         }
-        if constexpr (PAIRED && one_byte_codes(SRC)) CodeIO<SRC>::template load8<LPB / 2>(dt, lbase, j, mc, vc);
+        if constexpr (PAIRED && one_byte_codes(SRC)) craw = CodeIO<SRC>::raw8(dt, lbase, j);
 #pragma unroll
         for (int e = 0; e < EPL; ++e) ok[e] = true;
     } else {
@@ -826,6 +847,11 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
             }
         }
     }
+    sm = block_bcast<LPB>(sm);
+    sv = block_bcast<LPB>(sv);
+    vmin = block_bcast<LPB>(vmin);
+    if constexpr (FULL && C::QPL > 0 && PAIRED && one_byte_codes(SRC))
+        CodeIO<SRC>::template decode8<LPB / 2>(craw, j, mc, vc);
     if constexpr (narrows_codes<SRC, DST>()) {
         constexpr float lo = DST == ST_S16 ? -32768.0f : -128.0f;
         constexpr float hi = DST == ST_S16 ? 32767.0f : 127.0f;
@@ -1330,7 +1356,7 @@ __global__ __launch_bounds__(Cfg<LOG2B>::THREADS) void mdq_step_kernel(const Mdq
     // staged tiles: the lines of p and grads, then the p stores (tiles of several waves: the p stores)
     constexpr int GBK = GT == GT_F32 ? 4 : 2;
     __shared__ __attribute__((aligned(16)))
-    float pst_s[!VIEWS || C::QPL == 0 ? 1 : staged_mode<SR, LOG2B>() ? staged_lds_bytes(C::TILE, GBK) / 4 : C::TILE];
+    float pst_s[!VIEWS || C::QPL == 0 ? 1 : staged_mode<SRC, DST, SR, LOG2B>() ? staged_lds_bytes(C::TILE, GBK) / 4 : C::TILE];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const unsigned grid = gridDim.x, b = blockIdx.x;
@@ -1361,7 +1387,7 @@ __global__ __launch_bounds__(Cfg<LOG2B>::THREADS) void mdq_step_kernel(const Mdq
         if (inside && (d.flags & DF_ALIGNED) && (C::WAVES > 1 || (d.flags & DF_LINES))) {
             mdq_step_tile<SRC, DST, GT, LOG2B, SR, true, TILE_VECTOR>(d, tl, lane, wave, lut_s, xw_s, pst_s, sa, prof_on, pa);
         } else if (C::QPL > 0 && inside && (d.flags & DF_CODES_ALIGNED)) {
-            if constexpr (staged_mode<SR, LOG2B>())
+            if constexpr (staged_mode<SRC, DST, SR, LOG2B>())
                 mdq_step_tile<SRC, DST, GT, LOG2B, SR, true, TILE_STAGED>(d, tl, lane, wave, lut_s, xw_s, pst_s, sa, prof_on, pa);
             else if constexpr (C::QPL > 0)
                 mdq_step_tile<SRC, DST, GT, LOG2B, SR, true, TILE_UNALIGNED_PG>(d, tl, lane, wave, lut_s, xw_s, pst_s, sa, prof_on, pa);
