@@ -15,7 +15,13 @@
  * staging buffers that later calls reuse (or launch from a device copy of an
  * identical table, see stq_step_table_uploads), so they refuse
  * (STQ_ERR_INVALID, nothing queued) a stream that is capturing a HIP graph: a
- * replay of such a capture would launch with another call's descriptors.
+ * replay of such a capture would launch with another call's descriptors.  The
+ * exception is a step over one tensor that keeps its storage
+ * (stq_fused_mdq_adamw, or stq_multi_tensor_mdq_adamw with one tensor with
+ * elements): on a capturing stream its descriptor travels as a kernel
+ * argument, so the graph records one kernel node that each replay runs with
+ * the captured pointers and constants (step, lr, seed ...), as a captured
+ * launch of the reference's kernel would (since STQ_ABI_VERSION 4).
  */
 #ifndef STQUANT_HIP_H
 #define STQUANT_HIP_H
@@ -26,7 +32,7 @@
 extern "C" {
 #endif
 
-#define STQ_ABI_VERSION 3
+#define STQ_ABI_VERSION 4
 
 enum stq_status {
     STQ_OK = 0,
@@ -78,6 +84,8 @@ enum stq_rounding {
  * Extensions beyond the reference: grad dtype, rounding / seed / tensor_id
  * (stochastic rounding stream), the stream argument, and 64-bit numel.
  * Storage dispatch and its error message follow stquant_kernel.cu:430-464.
+ * A call on a stream that is capturing a HIP graph is captured as one kernel
+ * node (see the top of this file).
  */
 int stq_fused_mdq_adamw(float *p, const void *grad, int grad_dtype, int64_t grad_numel,
                         int64_t numel,

@@ -267,20 +267,33 @@ int take_slot(DevCtx *ctx, size_t need, Slot **out)
     return STQ_OK;
 }
 
-// Descriptor tables are uploaded from a ring of staging slots that later
-// calls refill, so a call captured into a HIP graph would, on replay, launch
-// with whatever another call left in its slot.  Every entry point that uploads
-// refuses a capturing stream before any slot, event or device work.
-int refuse_capture(hipStream_t stream)
+// Whether `stream` is capturing a HIP graph.
+int is_capturing(hipStream_t stream, bool *capturing)
 {
     hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
     const hipError_t e = hipStreamIsCapturing(stream, &cs);
     if (e != hipSuccess) return hip_fail(e, "hipStreamIsCapturing");
-    if (cs != hipStreamCaptureStatusNone)
+    *capturing = cs != hipStreamCaptureStatusNone;
+    return STQ_OK;
+}
+
+// Descriptor tables are uploaded from a ring of staging slots that later
+// calls refill, so a call captured into a HIP graph would, on replay, launch
+// with whatever another call left in its slot.  Every entry point that uploads
+// a table refuses a capturing stream before any slot, event or device work
+// (a step over one tensor that keeps its storage is captured instead, with its
+// descriptor as a kernel argument: upload_and_launch).
+int refuse_capture(hipStream_t stream)
+{
+    bool capturing = false;
+    const int rc = is_capturing(stream, &capturing);
+    if (rc != STQ_OK) return rc;
+    if (capturing)
         return fail(STQ_ERR_INVALID,
                     "the stream is capturing a HIP graph: this library uploads each call's descriptor table "
                     "from staging buffers that later calls reuse, so a replay would step other tensors; "
-                    "call it outside graph capture");
+                    "call it outside graph capture (a step over one tensor, as fused_mdq_adamw, can be "
+                    "captured)");
     return STQ_OK;
 }
 
@@ -370,6 +383,19 @@ hipError_t launch_step(const MdqDesc *dd, int nd, int src, int storage, int grad
     }
 }
 
+// Launches the step kernel over one tensor whose descriptor d (tile_begin 0) travels as a
+// kernel argument.
+hipError_t launch_step_one(const MdqDesc &d, int storage, int grad_dt, int log2b, bool sr, int64_t total_tiles,
+                           unsigned long long *prof, const mdq::StepArgs &sa, hipStream_t stream)
+{
+    switch (storage) {
+    case mdq::ST_P4: return mdq::launch_one_p4(d, total_tiles, grad_dt, log2b, sr, prof, sa, stream);
+    case mdq::ST_S8: return mdq::launch_one_s8(d, total_tiles, grad_dt, log2b, sr, prof, sa, stream);
+    case mdq::ST_S16: return mdq::launch_one_s16(d, total_tiles, grad_dt, log2b, sr, prof, sa, stream);
+    default: return mdq::launch_one_s32(d, total_tiles, grad_dt, log2b, sr, prof, sa, stream);
+    }
+}
+
 // The same bits (so +0 / -0 and NaN patterns count as different).
 bool same_bits(float a, float b) { return std::memcmp(&a, &b, sizeof a) == 0; }
 
@@ -384,15 +410,18 @@ bool same_bits(float a, float b) { return std::memcmp(&a, &b, sizeof a) == 0; }
 // upload (the copy and, for large launches, the wait for the copy stream
 // leave the GPU idle between back-to-back steps).  `storage` is the code
 // storage the kernel writes; it reads `src_storage` (the same, except on a
-// storage-changing step).
+// storage-changing step).  On a stream that is capturing a HIP graph, a step over
+// one tensor that keeps its storage launches with its descriptor as a kernel
+// argument (mdq_step_kernel_one: no upload, so the graph holds a plain kernel
+// node that replays with the captured pointers and constants, as a captured
+// launch of the reference's kernel would); other calls are refused.
 int upload_and_launch(const MdqDesc *descs, size_t n, int src_storage, int storage, int grad_dt, int log2b,
                       bool sr, int64_t total_tiles, unsigned long long *prof, uint64_t seed, hipStream_t stream)
 {
-    int rc = refuse_capture(stream);
+    bool capturing = false;
+    int rc = is_capturing(stream, &capturing);
     if (rc != STQ_OK) return rc;
-    DevCtx *ctx = nullptr;
-    rc = get_ctx(&ctx);
-    if (rc != STQ_OK) return rc;
+    if (capturing && !(n == 1 && src_storage == storage)) return refuse_capture(stream);
     mdq::StepArgs sa{seed, 0.0f, 0.0f, 0u, 0u};
     bool uniform = n > 0;
     for (size_t i = 1; i < n && uniform; ++i)
@@ -404,6 +433,13 @@ int upload_and_launch(const MdqDesc *descs, size_t n, int src_storage, int stora
         sa.step = descs[0].step;
         sa.uniform = 1u;
     }
+    if (capturing) {
+        const hipError_t e = launch_step_one(descs[0], storage, grad_dt, log2b, sr, total_tiles, prof, sa, stream);
+        return e == hipSuccess ? STQ_OK : hip_fail(e, "kernel launch");
+    }
+    DevCtx *ctx = nullptr;
+    rc = get_ctx(&ctx);
+    if (rc != STQ_OK) return rc;
     const size_t need = n * (sizeof(MdqDesc) + sizeof(long long));
     thread_local std::vector<char> table;
     table.resize(need);

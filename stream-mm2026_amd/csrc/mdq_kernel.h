@@ -1324,54 +1324,44 @@ __device__ __forceinline__ void mdq_step_tile(const MdqDesc &d, int64_t tl, int 
 // Workgroups of the last, partial round of 8 chunks take tile b (a bijection
 // on [0, grid)).  Same-allocation A/B on the LLaMA set against one contiguous
 // eighth per XCD: 4-bit 12.93 vs 13.26 ms, 8-bit level, GPT-2 small 0.282 vs
-// 0.297 ms; chunks of 1, 8, 32, 96 or 512+ tiles were slower.  The tile's
-// tensor is the largest t with
-// tile_begin[t] <= tile (tile_begin: compact int64 copy of the descriptors'
-// tile starts, so the ~log2(n_desc) dependent scalar loads hit a few cache
-// lines).  Profiling (prof != null) samples every 64th tile; only the phase
-// ratios of the cycle sums are meaningful.
-// VIEWS: the variant with the staged tile modes (and their LDS), which the host
-// launches only when some tensor with whole tiles and aligned codes has p or
-// grads off their 128-byte lines; the other variant has the vector and guarded
-// modes alone, so aligned launches run code without the staged paths' register
-// pressure (LLaMA-7B 4-bit stochastic: 13.71 ms with them in one kernel, 13.36
-// without, same box).
-template <int SRC, int DST, int GT, int LOG2B, bool SR, bool VIEWS>
-__global__ __launch_bounds__(Cfg<LOG2B>::THREADS) void mdq_step_kernel(const MdqDesc *__restrict__ descs,
-                                                                      const long long *__restrict__ tile_begin,
-                                                                      int n_desc,
-                                                                      unsigned long long *__restrict__ prof,
-                                                                      const StepArgs sa)
+// 0.297 ms; chunks of 1, 8, 32, 96 or 512+ tiles were slower.
+template <int LOG2B>
+__device__ __forceinline__ long long xcd_tile()
 {
     using C = Cfg<LOG2B>;
-    // Occupancy cap at 7 waves per SIMD: the clobber reserves v0..v71, so the
-    // register file never holds 8 of these waves, whatever the compiler's
-    // count.  With one contiguous eighth of the tiles per XCD, 8 waves ran the
-    // LLaMA 4-bit step 1 % slower (same-allocation A/B 13.36 vs 13.23 ms); with
-    // the chunked tile order below the two are level (+-0.3 %).
-    asm volatile("" ::: "v71");
-    constexpr bool USE_LUT = (SRC == ST_P4) && C::B >= 32;
-    __shared__ float lut_s[USE_LUT ? C::TB * 16 : 1];
-    __shared__ int32_t xw_s[6];
-    // staged tiles: the lines of p and grads, then the p stores (tiles of several waves: the p stores)
-    constexpr int GBK = GT == GT_F32 ? 4 : 2;
-    __shared__ __attribute__((aligned(16)))
-    float pst_s[!VIEWS || C::QPL == 0 ? 1 : staged_mode<SRC, DST, SR, LOG2B>() ? staged_lds_bytes(C::TILE, GBK) / 4 : C::TILE];
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
     const unsigned grid = gridDim.x, b = blockIdx.x;
     constexpr unsigned K = C::TILE >= 65536 ? 1u : 65536u / C::TILE;   // tiles per chunk
     const unsigned j = b >> 3, x = b & 7u;
-    const long long tile = b < grid / (8u * K) * (8u * K) ? (long long)((j / K) * 8u + x) * K + (j % K)
-                                                          : (long long)b;
-    int lo = 0, hi = n_desc - 1;
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (tile_begin[mid] <= tile) lo = mid;
-        else hi = mid - 1;
-    }
-    const MdqDesc &d = descs[__builtin_amdgcn_readfirstlane(lo)];
-    const long long tl = tile - d.tile_begin;
+    return b < grid / (8u * K) * (8u * K) ? (long long)((j / K) * 8u + x) * K + (j % K) : (long long)b;
+}
+
+// LDS of one tile: the exp table of packed 4-bit codes, the cross-wave reduction slots, and
+// for staged tiles the lines of p and grads, then the p stores (tiles of several waves: the
+// p stores).
+template <int SRC, int DST, int GT, int LOG2B, bool SR, bool VIEWS>
+struct StepLds {
+    using C = Cfg<LOG2B>;
+    static constexpr int LUT = (SRC == ST_P4) && C::B >= 32 ? C::TB * 16 : 1;
+    static constexpr int PST = !VIEWS || C::QPL == 0 ? 1
+                               : staged_mode<SRC, DST, SR, LOG2B>() ? staged_lds_bytes(C::TILE, GT == GT_F32 ? 4 : 2) / 4
+                                                                    : C::TILE;
+};
+
+// Tile `tile` (tl within its tensor d) in the mode its tensor's flags allow.  Profiling
+// (prof != null) samples every 64th tile; only the phase ratios of the cycle sums are
+// meaningful.  VIEWS: the variant with the staged tile modes (and their LDS), which the host
+// launches only when some tensor with whole tiles and aligned codes has p or grads off their
+// 128-byte lines; the other variant has the vector and guarded modes alone, so aligned
+// launches run code without the staged paths' register pressure (LLaMA-7B 4-bit stochastic:
+// 13.71 ms with them in one kernel, 13.36 without, same box).
+template <int SRC, int DST, int GT, int LOG2B, bool SR, bool VIEWS>
+__device__ __forceinline__ void mdq_step_tile_any(const MdqDesc &d, long long tile, long long tl, float *lut_s,
+                                                  int32_t *xw_s, float *pst_s, unsigned long long *prof,
+                                                  const StepArgs &sa)
+{
+    using C = Cfg<LOG2B>;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
     const bool prof_on = prof != nullptr && (tile & 63) == 0;
     ProfAcc pa = {{0, 0, 0, 0, 0}};
     const bool inside = (tl + 1) * C::TILE <= d.numel;
@@ -1399,6 +1389,55 @@ __global__ __launch_bounds__(Cfg<LOG2B>::THREADS) void mdq_step_kernel(const Mdq
 #pragma unroll
         for (int s = 0; s < 5; ++s) atomicAdd(prof + s, pa.c[s]);
     }
+}
+
+// Occupancy cap at 7 waves per SIMD in both kernels below: the clobber reserves v0..v71, so
+// the register file never holds 8 of these waves, whatever the compiler's count.  With one
+// contiguous eighth of the tiles per XCD, 8 waves ran the LLaMA 4-bit step 1 % slower
+// (same-allocation A/B 13.36 vs 13.23 ms); with the chunked tile order the two are level
+// (+-0.3 %).
+
+// The launch over a descriptor table: the tile's tensor is the largest t with
+// tile_begin[t] <= tile (tile_begin: compact int64 copy of the descriptors' tile starts, so
+// the ~log2(n_desc) dependent scalar loads hit a few cache lines).
+template <int SRC, int DST, int GT, int LOG2B, bool SR, bool VIEWS>
+__global__ __launch_bounds__(Cfg<LOG2B>::THREADS) void mdq_step_kernel(const MdqDesc *__restrict__ descs,
+                                                                      const long long *__restrict__ tile_begin,
+                                                                      int n_desc,
+                                                                      unsigned long long *__restrict__ prof,
+                                                                      const StepArgs sa)
+{
+    asm volatile("" ::: "v71");
+    using L = StepLds<SRC, DST, GT, LOG2B, SR, VIEWS>;
+    __shared__ float lut_s[L::LUT];
+    __shared__ int32_t xw_s[6];
+    __shared__ __attribute__((aligned(16))) float pst_s[L::PST];
+    const long long tile = xcd_tile<LOG2B>();
+    int lo = 0, hi = n_desc - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (tile_begin[mid] <= tile) lo = mid;
+        else hi = mid - 1;
+    }
+    const MdqDesc &d = descs[__builtin_amdgcn_readfirstlane(lo)];
+    mdq_step_tile_any<SRC, DST, GT, LOG2B, SR, VIEWS>(d, tile, tile - d.tile_begin, lut_s, xw_s, pst_s, prof, sa);
+}
+
+// The launch over one tensor whose descriptor is a kernel argument (tile_begin 0): no table
+// in device memory, so a call on a stream that is capturing a HIP graph records a plain
+// kernel node.  The variant with every tile mode.
+template <int SRC, int GT, int LOG2B, bool SR>
+__global__ __launch_bounds__(Cfg<LOG2B>::THREADS) void mdq_step_kernel_one(const MdqDesc d,
+                                                                          unsigned long long *__restrict__ prof,
+                                                                          const StepArgs sa)
+{
+    asm volatile("" ::: "v71");
+    using L = StepLds<SRC, SRC, GT, LOG2B, SR, true>;
+    __shared__ float lut_s[L::LUT];
+    __shared__ int32_t xw_s[6];
+    __shared__ __attribute__((aligned(16))) float pst_s[L::PST];
+    const long long tile = xcd_tile<LOG2B>();
+    mdq_step_tile_any<SRC, SRC, GT, LOG2B, SR, true>(d, tile, tile, lut_s, xw_s, pst_s, prof, sa);
 }
 
 }  // namespace mdq

@@ -14,6 +14,13 @@ hipError_t launch_s8(const MdqDesc *, int, long long, int, int, bool, unsigned l
 hipError_t launch_s16(const MdqDesc *, int, long long, int, int, bool, unsigned long long *, const StepArgs &, bool, hipStream_t);
 hipError_t launch_s32(const MdqDesc *, int, long long, int, int, bool, unsigned long long *, const StepArgs &, bool, hipStream_t);
 
+// One tensor whose descriptor travels as a kernel argument (no table in device memory: the
+// launch of a call on a stream that captures a HIP graph).
+hipError_t launch_one_p4(const MdqDesc &, long long, int, int, bool, unsigned long long *, const StepArgs &, hipStream_t);
+hipError_t launch_one_s8(const MdqDesc &, long long, int, int, bool, unsigned long long *, const StepArgs &, hipStream_t);
+hipError_t launch_one_s16(const MdqDesc &, long long, int, int, bool, unsigned long long *, const StepArgs &, hipStream_t);
+hipError_t launch_one_s32(const MdqDesc &, long long, int, int, bool, unsigned long long *, const StepArgs &, hipStream_t);
+
 // Storage-changing steps (codes read in storage src, written in the destination
 // storage of the function name): block sizes 2^TRANSITION_LOG2B_MIN ..
 // 2^TRANSITION_LOG2B_MAX; src must differ from the destination.

@@ -54,7 +54,7 @@ EXPORTED_SYMBOLS = (
 
 
 # STQ_ABI_VERSION of include/stquant_hip.h this package is written against
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 
 class StqTensor(ctypes.Structure):

@@ -27,7 +27,7 @@ def test_exports_every_declared_symbol():
     for name in names:
         assert hasattr(L, name), name
     assert set(names) == set(_capi.EXPORTED_SYMBOLS)
-    assert L.stq_abi_version() == _capi.ABI_VERSION == 3
+    assert L.stq_abi_version() == _capi.ABI_VERSION == 4
 
 
 FAKE = 0x1000  # never dereferenced: every call below fails argument checks first

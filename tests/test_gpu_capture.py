@@ -1,7 +1,15 @@
-"""HIP graph capture is refused: every entry point that uploads a descriptor table returns
-STQ_ERR_INVALID while its stream is capturing, before it queues anything, so no replay can
-launch with another call's descriptors.  The captures are ended and never replayed; calls
-after them work as before."""
+"""HIP graph capture.
+
+A step over one tensor that keeps its storage (the reference's ``fused_mdq_adamw``, or a list of
+one) is captured as one kernel node whose descriptor is a kernel argument: each replay steps the
+captured tensors again with the captured constants, as a captured launch of the reference's kernel
+does.  Replays, with eager work and synchronisations between them, are checked bit for bit against
+the same calls made eagerly on a twin state, after every replay.
+
+Every other entry point uploads a descriptor table from staging buffers that later calls reuse, so
+it refuses a capturing stream: STQ_ERR_INVALID before anything is queued.  Those captures are ended
+and never replayed; calls after them work as before."""
+import numpy as np
 import pytest
 import torch
 
@@ -20,13 +28,13 @@ def _state(n=4096, B=128):
     return [p, g, m, v, torch.zeros(nb, device=DEV), torch.zeros(nb, device=DEV), torch.full((nb,), -20.0, device=DEV)]
 
 
-def _calls(t):
+def _calls(t, t2):
     p, g, m, v, sm, sv, vm = t
-    entry = mdq_hip.TensorState(p, g, m, v, sm, sv, vm, 1, 16, 1e-3, 0.9, 0.999, 1e-8, 0.01)
+    entries = [mdq_hip.TensorState(*x, 1, 16, 1e-3, 0.9, 0.999, 1e-8, 0.01) for x in (t, t2)]
     nm, nv = mdq_hip.empty_codes(m, mdq_hip.STORE_S8)
     return {
-        "fused_step": lambda: mdq_hip.fused_step(p, g, m, v, sm, sv, vm, 0.9, 0.999, 1e-3, 0.01, 1e-8, 1, 16, 128),
-        "multi_tensor_step": lambda: mdq_hip.multi_tensor_step([entry], 128),
+        "multi_tensor_step": lambda: mdq_hip.multi_tensor_step(entries, 128),
+        "multi_tensor_step_noalloc": lambda: mdq_hip.MultiTensorPlan(entries[:1], 128).run(noalloc=True),
         "multi_tensor_restore": lambda: mdq_hip.multi_tensor_restore(
             [mdq_hip.TensorState(p, g, m, v, sm, sv, vm, 1, 8, 1e-3, 0.9, 0.999, 1e-8, 0.01)], [(nm, nv)], 128),
         "grad_stats": lambda: mdq_hip.grad_stats([g]),
@@ -34,13 +42,13 @@ def _calls(t):
     }
 
 
-@pytest.mark.parametrize("name", ["fused_step", "multi_tensor_step", "multi_tensor_restore", "grad_stats",
-                                  "convert_codes"])
+@pytest.mark.parametrize("name", ["multi_tensor_step", "multi_tensor_step_noalloc", "multi_tensor_restore",
+                                  "grad_stats", "convert_codes"])
 def test_capture_is_refused(name):
     print(f"case: capture refusal {name}", flush=True)
-    t = _state()
-    before = [x.clone() for x in t]
-    call = _calls(t)[name]
+    t, t2 = _state(), _state()
+    before = [x.clone() for x in t + t2]
+    call = _calls(t, t2)[name]
     torch.cuda.synchronize()
     side = torch.cuda.Stream()
     graph = torch.cuda.CUDAGraph()
@@ -55,9 +63,77 @@ def test_capture_is_refused(name):
             graph.capture_end()
     torch.cuda.synchronize()
     assert err is not None and "capturing a HIP graph" in err, err
-    for a, b in zip(t, before):                  # nothing ran
+    for a, b in zip(t + t2, before):             # nothing ran
         assert torch.equal(a, b)
     del graph
     # outside capture the same call works
     call()
     torch.cuda.synchronize()
+
+
+CODE_DTYPES = {4: (torch.uint8, None), 8: (torch.int8, torch.uint8), 16: (torch.int16, torch.uint16)}
+
+
+def _one_tensor(n, B, bits, offset, seed):
+    """Two identical copies of one tensor's state; p and the grads views at `offset` elements
+    into their buffers (offset 5: inside a 128-byte line, the staged tiles)."""
+    gen = torch.Generator(device=DEV).manual_seed(seed)
+    nb = (n + B - 1) // B
+    mdt, vdt = CODE_DTYPES[bits]
+    pb = torch.randn(n + offset, device=DEV, generator=gen) * 0.02
+    if bits == 4:
+        m = torch.randint(0, 256, (n,), device=DEV, generator=gen).to(torch.uint8)
+        v = torch.empty(0, dtype=torch.uint8, device=DEV)
+    else:
+        lo = torch.iinfo(mdt).min // 2
+        m = torch.randint(lo, -lo, (n,), device=DEV, generator=gen).to(mdt)
+        v = torch.randint(0, 2 * -lo, (n,), device=DEV, generator=gen).to(vdt)
+    sm = torch.rand(nb, device=DEV, generator=gen) * 1e-4
+    sv = torch.rand(nb, device=DEV, generator=gen)
+    vm = -20.0 + torch.rand(nb, device=DEV, generator=gen)
+    twins = []
+    for _ in range(2):
+        pbuf, gbuf = pb.clone(), torch.zeros(n + offset, device=DEV)
+        twins.append(dict(p=pbuf[offset:], g=gbuf[offset:], m=m.clone(), v=v.clone(), sm=sm.clone(),
+                          sv=sv.clone(), vm=vm.clone(), keep=(pbuf, gbuf)))
+    return twins
+
+
+def _step(s, B, bits, step, rounding):
+    mdq_hip.fused_step(s["p"], s["g"], s["m"], s["v"], s["sm"], s["sv"], s["vm"], 0.9, 0.999, 1e-3, 0.01, 1e-8,
+                       step, bits, B, rounding=rounding, seed=11, tensor_id=4)
+
+
+@pytest.mark.parametrize("bits", [4, 8, 16])
+@pytest.mark.parametrize("rounding", ["nearest", "stochastic"])
+@pytest.mark.parametrize("B,n,offset", [(128, 512 * 40 + 77, 0), (64, 512 * 40, 5), (256, 512 * 12 + 3, 5)])
+def test_one_tensor_step_is_captured_and_replays(bits, rounding, B, n, offset):
+    print(f"case: captured one-tensor step bits={bits} {rounding} B={B} n={n} offset={offset}", flush=True)
+    cap, ref = _one_tensor(n, B, bits, offset, seed=bits + B + offset)
+    step = 7
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    uploads = mdq_hip.step_table_uploads()
+    with torch.cuda.stream(side):
+        graph.capture_begin()
+        _step(cap, B, bits, step, rounding)        # recorded, not run
+        graph.capture_end()
+    torch.cuda.synchronize()
+    assert mdq_hip.step_table_uploads() == uploads, "the captured call uploaded a descriptor table"
+    rng = np.random.default_rng(n + bits)
+    for r in range(4):
+        grads = torch.from_numpy((rng.standard_normal(n) * 1e-3).astype(np.float32)).to(DEV)
+        cap["g"].copy_(grads)
+        ref["g"].copy_(grads)
+        torch.cuda.synchronize()
+        graph.replay()
+        _step(ref, B, bits, step, rounding)        # eager, through the descriptor table
+        torch.cuda.synchronize()
+        for k in ("p", "m", "v", "sm", "sv", "vm"):
+            assert torch.equal(cap[k].view(torch.uint8), ref[k].view(torch.uint8)), (r, k)
+        for buf_c, buf_r in zip(cap["keep"], ref["keep"]):   # the padding in front of the views
+            assert torch.equal(buf_c[:offset], buf_r[:offset])
+        print(f"replay {r}: bit-identical to the eager call", flush=True)
+    del graph
