@@ -24,9 +24,13 @@ def pytest_terminal_summary(terminalreporter):
     ratios = [s["min_update_ratio_over"] for _, s in recs if s["min_update_ratio_over"] is not None]
     tr = terminalreporter
     tr.section("parameter error vs the oracle (bar |dp| <= 2^-20 |update| + 2^-22 |p'|)")
+    zero = sum(s.get("zero_target", 0) for _, s in recs)
     tr.write_line(f"{len(recs)} comparisons, {n:,} elements: {100 * ident:.3f} % bit-identical, "
-                  f"max {max(s['max_ulps'] for _, s in recs)} ulp, max |dp|/|p'| "
+                  f"max {max(s['max_ulps'] for _, s in recs)} ulp, max |dp|/|p'| (p' != 0) "
                   f"{max(s['rel_max'] for _, s in recs):.2e}, max bar use {max(s['bar_use'] for _, s in recs):.3f}")
+    if zero:
+        tr.write_line(f"p' = 0 in the oracle with dp != 0: {zero:,} elements, max |dp| "
+                      f"{max(s.get('zero_target_max_abs', 0.0) for _, s in recs):.2e} (within the bar's update term)")
     tr.write_line(f"elements above 1e-6 relative: {int(round(over)):,} ({100 * over / max(n, 1):.4f} %), "
                   f"every one with |update| >= {min(ratios) if ratios else float('nan'):.2f} |p'| "
                   f"(a step through or next to zero)")

@@ -41,8 +41,11 @@ def param_error_stats(got, want, prev):
     err = np.abs(g64 - w64)
     upd = np.abs(w64 - pv.astype(np.float64))
     bar = UPDATE_TERM * upd + PARAM_TERM * np.abs(w64) + FLOOR
+    # relative error where the oracle's p' is nonzero; a p' of exactly 0 (the step cancels p) has
+    # no relative error, and its absolute error is reported on its own (it is held to the bar too)
+    zero_want = (w64 == 0) & (err > 0)
     with np.errstate(divide="ignore", invalid="ignore"):
-        rel = np.where(err == 0, 0.0, err / np.abs(w64))
+        rel = np.where((err == 0) | zero_want, 0.0, err / np.abs(w64))
     # ulp distance on the ordered integer line of float32 bit patterns
     gi = g.view(np.int32).astype(np.int64)
     wi = w.view(np.int32).astype(np.int64)
@@ -65,6 +68,8 @@ def param_error_stats(got, want, prev):
         # (implied by the bar wherever |p'| is well above FLT_MIN * 2^20)
         min_update_ratio_over=(float(np.min(upd[over & big] / np.abs(w64[over & big])))
                                if (over & big).any() else None),
+        zero_target=int(np.count_nonzero(zero_want)),
+        zero_target_max_abs=float(err[zero_want].max()) if zero_want.any() else 0.0,
         bar_use=float(np.max(err / bar)) if n else 0.0,
         worst=int(np.argmax(err / bar)) if n else -1,
     )
@@ -74,9 +79,11 @@ def format_stats(s, label=""):
     over = s["share_rel_over_1e6"]
     tail = (f"; above 1e-6 relative: {100 * over:.4f} % of elements, each with |update| >= "
             f"{s['min_update_ratio_over']:.2f} |p'|" if over else "; none above 1e-6 relative")
+    zero = (f"; p' = 0 in the oracle with dp != 0: {s['zero_target']} elements, max |dp| "
+            f"{s['zero_target_max_abs']:.2e}" if s["zero_target"] else "")
     return (f"params{(' ' + label) if label else ''}: {s['n']:,} elements, {100 * s['identical']:.3f} % bit-identical, "
-            f"max {s['max_ulps']} ulp; |dp|/|p'| median {s['rel_q50']:.2e}, 99 % {s['rel_q99']:.2e}, "
-            f"99.9 % {s['rel_q999']:.2e}, max {s['rel_max']:.2e}{tail}; bar use {s['bar_use']:.3f}")
+            f"max {s['max_ulps']} ulp; |dp|/|p'| (p' != 0) median {s['rel_q50']:.2e}, 99 % {s['rel_q99']:.2e}, "
+            f"99.9 % {s['rel_q999']:.2e}, max {s['rel_max']:.2e}{tail}{zero}; bar use {s['bar_use']:.3f}")
 
 
 def assert_param_bar(got, want, prev, label="", quiet=False):
