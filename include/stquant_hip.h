@@ -18,10 +18,10 @@
  * replay of such a capture would launch with another call's descriptors.  The
  * exception is a step over one tensor that keeps its storage
  * (stq_fused_mdq_adamw, or stq_multi_tensor_mdq_adamw with one tensor with
- * elements): on a capturing stream its descriptor travels as a kernel
- * argument, so the graph records one kernel node that each replay runs with
- * the captured pointers and constants (step, lr, seed ...), as a captured
- * launch of the reference's kernel would (since STQ_ABI_VERSION 4).
+ * elements): its descriptor travels as a kernel argument (no table), so on a
+ * capturing stream the graph records one kernel node that each replay runs
+ * with the captured pointers and constants (step, lr, seed ...), as a
+ * captured launch of the reference's kernel would (since STQ_ABI_VERSION 4).
  */
 #ifndef STQUANT_HIP_H
 #define STQUANT_HIP_H

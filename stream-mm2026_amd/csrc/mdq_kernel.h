@@ -1424,8 +1424,10 @@ __global__ __launch_bounds__(Cfg<LOG2B>::THREADS) void mdq_step_kernel(const Mdq
 }
 
 // The launch over one tensor whose descriptor is a kernel argument (tile_begin 0): no table
-// in device memory, so a call on a stream that is capturing a HIP graph records a plain
-// kernel node.  The variant with every tile mode.
+// in device memory to upload or look up (the flat 4,194,304-element step 14.6 -> 11.9 us per
+// call), and a call on a stream that is capturing a HIP graph records a plain kernel node.
+// The variant with every tile mode (a one-tensor LLaMA-size step runs level with the
+// table-driven kernel).
 template <int SRC, int GT, int LOG2B, bool SR>
 __global__ __launch_bounds__(Cfg<LOG2B>::THREADS) void mdq_step_kernel_one(const MdqDesc d,
                                                                           unsigned long long *__restrict__ prof,

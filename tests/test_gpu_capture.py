@@ -3,8 +3,9 @@
 A step over one tensor that keeps its storage (the reference's ``fused_mdq_adamw``, or a list of
 one) is captured as one kernel node whose descriptor is a kernel argument: each replay steps the
 captured tensors again with the captured constants, as a captured launch of the reference's kernel
-does.  Replays, with eager work and synchronisations between them, are checked bit for bit against
-the same calls made eagerly on a twin state, after every replay.
+does.  Replays, with eager work and synchronisations between them, are checked bit for bit after
+every replay against the same step made eagerly on a twin state in a launch over two tensors, which
+takes the descriptor-table kernel: the one-tensor kernel against the table-driven one.
 
 Every other entry point uploads a descriptor table from staging buffers that later calls reuse, so
 it refuses a capturing stream: STQ_ERR_INVALID before anything is queued.  Those captures are ended
@@ -104,12 +105,24 @@ def _step(s, B, bits, step, rounding):
                        step, bits, B, rounding=rounding, seed=11, tensor_id=4)
 
 
+def _entry(s, bits, step, tensor_id):
+    return mdq_hip.TensorState(s["p"], s["g"], s["m"], s["v"], s["sm"], s["sv"], s["vm"], step, bits,
+                               1e-3, 0.9, 0.999, 1e-8, 0.01, tensor_id)
+
+
+def _step_in_a_table(s, other, B, bits, step, rounding):
+    """The same step as _step, in a launch over two tensors (the descriptor-table kernel)."""
+    mdq_hip.multi_tensor_step([_entry(s, bits, step, 4), _entry(other, bits, step, 5)], B,
+                              rounding=rounding, seed=11)
+
+
 @pytest.mark.parametrize("bits", [4, 8, 16])
 @pytest.mark.parametrize("rounding", ["nearest", "stochastic"])
 @pytest.mark.parametrize("B,n,offset", [(128, 512 * 40 + 77, 0), (64, 512 * 40, 5), (256, 512 * 12 + 3, 5)])
 def test_one_tensor_step_is_captured_and_replays(bits, rounding, B, n, offset):
     print(f"case: captured one-tensor step bits={bits} {rounding} B={B} n={n} offset={offset}", flush=True)
     cap, ref = _one_tensor(n, B, bits, offset, seed=bits + B + offset)
+    other = _one_tensor(300, B, bits, 0, seed=99)[0]
     step = 7
     torch.cuda.synchronize()
     side = torch.cuda.Stream()
@@ -129,11 +142,11 @@ def test_one_tensor_step_is_captured_and_replays(bits, rounding, B, n, offset):
         ref["g"].copy_(grads)
         torch.cuda.synchronize()
         graph.replay()
-        _step(ref, B, bits, step, rounding)        # eager, through the descriptor table
+        _step_in_a_table(ref, other, B, bits, step, rounding)   # eager, the descriptor-table kernel
         torch.cuda.synchronize()
         for k in ("p", "m", "v", "sm", "sv", "vm"):
             assert torch.equal(cap[k].view(torch.uint8), ref[k].view(torch.uint8)), (r, k)
         for buf_c, buf_r in zip(cap["keep"], ref["keep"]):   # the padding in front of the views
             assert torch.equal(buf_c[:offset], buf_r[:offset])
-        print(f"replay {r}: bit-identical to the eager call", flush=True)
+        print(f"replay {r}: bit-identical to the eager table-driven step", flush=True)
     del graph
