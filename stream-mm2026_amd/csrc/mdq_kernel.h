@@ -1395,7 +1395,17 @@ __device__ __forceinline__ void mdq_step_tile_any(const MdqDesc &d, long long ti
 // the register file never holds 8 of these waves, whatever the compiler's count.  With one
 // contiguous eighth of the tiles per XCD, 8 waves ran the LLaMA 4-bit step 1 % slower
 // (same-allocation A/B 13.36 vs 13.23 ms); with the chunked tile order the two are level
-// (+-0.3 %).
+// (+-0.3 %).  Steps on int8 + uint8 codes are capped at 6 (v0..v79 reserved; the stochastic
+// ones already need 74-77 VGPRs): with nearest rounding, config 5 B = 64 / 128 / 256 0.953 ->
+// 0.934, 0.957 -> 0.939, 0.953 -> 0.941 ms, as packed views B = 128 0.967 -> 0.951 ms, LLaMA-7B
+// 15.34 -> 15.22 ms (same-allocation A/B).  Their waves wait on memory longer than the 4-bit
+// ones do, and one wave fewer per SIMD contends less.
+template <int SRC, int DST>
+__device__ __forceinline__ void occupancy_cap()
+{
+    if constexpr (SRC == ST_S8 && DST == ST_S8) asm volatile("" ::: "v79");
+    else asm volatile("" ::: "v71");
+}
 
 // The launch over a descriptor table: the tile's tensor is the largest t with
 // tile_begin[t] <= tile (tile_begin: compact int64 copy of the descriptors' tile starts, so
@@ -1407,7 +1417,7 @@ __global__ __launch_bounds__(Cfg<LOG2B>::THREADS) void mdq_step_kernel(const Mdq
                                                                       unsigned long long *__restrict__ prof,
                                                                       const StepArgs sa)
 {
-    asm volatile("" ::: "v71");
+    occupancy_cap<SRC, DST>();
     using L = StepLds<SRC, DST, GT, LOG2B, SR, VIEWS>;
     __shared__ float lut_s[L::LUT];
     __shared__ int32_t xw_s[6];
@@ -1433,7 +1443,7 @@ __global__ __launch_bounds__(Cfg<LOG2B>::THREADS) void mdq_step_kernel_one(const
                                                                           unsigned long long *__restrict__ prof,
                                                                           const StepArgs sa)
 {
-    asm volatile("" ::: "v71");
+    occupancy_cap<SRC, SRC>();
     using L = StepLds<SRC, SRC, GT, LOG2B, SR, true>;
     __shared__ float lut_s[L::LUT];
     __shared__ int32_t xw_s[6];
