@@ -1395,15 +1395,18 @@ __device__ __forceinline__ void mdq_step_tile_any(const MdqDesc &d, long long ti
 // the register file never holds 8 of these waves, whatever the compiler's count.  With one
 // contiguous eighth of the tiles per XCD, 8 waves ran the LLaMA 4-bit step 1 % slower
 // (same-allocation A/B 13.36 vs 13.23 ms); with the chunked tile order the two are level
-// (+-0.3 %).  Steps on int8 + uint8 codes are capped at 6 (v0..v79 reserved; the stochastic
-// ones already need 74-77 VGPRs): with nearest rounding, config 5 B = 64 / 128 / 256 0.953 ->
-// 0.934, 0.957 -> 0.939, 0.953 -> 0.941 ms, as packed views B = 128 0.967 -> 0.951 ms, LLaMA-7B
-// 15.34 -> 15.22 ms (same-allocation A/B).  Their waves wait on memory longer than the 4-bit
-// ones do, and one wave fewer per SIMD contends less.
-template <int SRC, int DST>
+// (+-0.3 %).  Steady steps on int8 + uint8 codes, and on packed 4-bit codes with nearest
+// rounding, are capped at 6 (v0..v79 reserved): their waves spend most of a tile waiting for its
+// loads, and one wave fewer per SIMD contends less.  Same-allocation A/B, nearest rounding:
+// 8-bit config 5 B = 64 / 128 / 256 -2.0 / -1.9 / -1.3 %, as packed views B = 128 -1.6 %,
+// LLaMA-7B -0.7 %; 4-bit (three boxes) LLaMA-7B -0.3 to -0.6 %, GPT-2 small -0.3 %, config 5
+// B = 64 -1.0 %, as packed views B = 128 -2.2 to -2.7 %.  Packed 4-bit codes with stochastic
+// rounding keep 7 (6: LLaMA-7B +0.8 %, views B = 64 +1.2 %); the stochastic 8-bit kernels need
+// 74-77 VGPRs and hold 6 anyway.
+template <int SRC, int DST, bool SR>
 __device__ __forceinline__ void occupancy_cap()
 {
-    if constexpr (SRC == ST_S8 && DST == ST_S8) asm volatile("" ::: "v79");
+    if constexpr ((SRC == ST_S8 && DST == ST_S8) || (SRC == ST_P4 && DST == ST_P4 && !SR)) asm volatile("" ::: "v79");
     else asm volatile("" ::: "v71");
 }
 
@@ -1417,7 +1420,7 @@ __global__ __launch_bounds__(Cfg<LOG2B>::THREADS) void mdq_step_kernel(const Mdq
                                                                       unsigned long long *__restrict__ prof,
                                                                       const StepArgs sa)
 {
-    occupancy_cap<SRC, DST>();
+    occupancy_cap<SRC, DST, SR>();
     using L = StepLds<SRC, DST, GT, LOG2B, SR, VIEWS>;
     __shared__ float lut_s[L::LUT];
     __shared__ int32_t xw_s[6];
@@ -1443,7 +1446,7 @@ __global__ __launch_bounds__(Cfg<LOG2B>::THREADS) void mdq_step_kernel_one(const
                                                                           unsigned long long *__restrict__ prof,
                                                                           const StepArgs sa)
 {
-    occupancy_cap<SRC, SRC>();
+    occupancy_cap<SRC, SRC, SR>();
     using L = StepLds<SRC, SRC, GT, LOG2B, SR, true>;
     __shared__ float lut_s[L::LUT];
     __shared__ int32_t xw_s[6];
