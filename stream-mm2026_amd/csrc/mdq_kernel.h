@@ -609,7 +609,7 @@ __device__ __forceinline__ float dequant_m(float code, float sm, float neg8sm)
 // LDS line by line (store_p_lines); codes move as in TILE_VECTOR.  Config 5 as
 // views back to back, B = 64: 64 % of HBM peak with the lanes' own element-aligned
 // vectors, 80 % staged, level with separate allocations.  TILE_UNALIGNED_PG (tiles
-// of more than one wave, and wider codes with stochastic rounding from B = 256 on,
+// of more than one wave, and 32-bit codes with stochastic rounding from B = 256 on,
 // staged_mode):
 // codes as in TILE_VECTOR, p and grads loaded as the lanes' vectors at element-aligned
 // addresses, and p stored through LDS when it does not start on a line.
@@ -620,14 +620,16 @@ enum TileMode : int { TILE_GUARDED = 0, TILE_VECTOR = 1, TILE_UNALIGNED_PG = 2, 
 // TILE_UNALIGNED_PG).  Same-allocation A/B on config 5 as packed views, stochastic
 // rounding, with the tile's loads all in flight before its first cross-lane DS
 // instruction (mdq_step_tile): staged against element-aligned vectors, B = 128 4-bit
-// 72.4 -> 78.7 % of HBM peak, 8-bit 74.2 -> 77.8 %; packed 4-bit codes B = 256 77.5 ->
-// 79.2 %, B = 512 78.6 -> 79.6 %; int8 + uint8 codes B = 256 level, B = 512 79.3 -> 78.5 %.
-// Nearest rounding: faster at every B.
+// 72.4 -> 78.7 % of HBM peak, 8-bit 74.2 -> 77.8 %; B = 256 4-bit 77.5 -> 79.2 %, 8-bit
+// 77.6 -> 78.8 / 77.7 -> 79.0 % (two boxes), 16-bit 77.5 -> 79.4 %; B = 512 4-bit 78.6 ->
+// 79.6 %, 8-bit 77.8 -> 78.9 %, 16-bit 77.5 -> 78.0 %; B = 1024 level; 32-bit codes B = 256
+// 75.0 -> 74.4 % (kept on element-aligned vectors from B = 256 on).  Nearest rounding:
+// faster at every B.
 template <int SRC, int DST, bool SR, int LOG2B>
 constexpr bool staged_mode()
 {
     return Cfg<LOG2B>::QPL > 0 && Cfg<LOG2B>::WAVES == 1 &&
-           (!SR || LOG2B <= 7 || (SRC == ST_P4 && DST == ST_P4));
+           (!SR || LOG2B <= 7 || (SRC != ST_S32 && DST != ST_S32));
 }
 
 // Bytes of LDS a one-wave staged tile uses for the lines of p (4 B per element) and

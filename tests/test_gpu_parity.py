@@ -286,15 +286,15 @@ def test_param_views_inside_a_cache_line(storage, bits, B, offset, gdt, full):
         c.check(p_prev)
 
 
-@pytest.mark.parametrize("storage,bits", [(orc.STORE_P4, 4), (orc.STORE_S8, 8), (orc.STORE_S16, 16)],
-                         ids=["p4", "s8", "s16"])
+@pytest.mark.parametrize("storage,bits", [(orc.STORE_P4, 4), (orc.STORE_S8, 8), (orc.STORE_S16, 16),
+                                          (orc.STORE_S32, 16)], ids=["p4", "s8", "s16", "s32"])
 @pytest.mark.parametrize("B,offset,gdt", [(32, 5, np.float32), (64, 31, "bf16"), (64, 4, np.float16),
                                           (128, 3, np.float32), (128, 30, "bf16"), (256, 17, "bf16"),
                                           (512, 12, np.float32), (1024, 9, np.float32)])
 def test_stochastic_rounding_on_param_views(storage, bits, B, offset, gdt):
-    """Stochastic rounding on params and grads that start inside a 128-byte line (staged lines up
-    to B = 128, and at every B for packed 4-bit codes; the lanes' element-aligned vectors above):
-    codes bit-exact, padding untouched."""
+    """Stochastic rounding on params and grads that start inside a 128-byte line (staged lines,
+    except for 32-bit storage from B = 256 on: the lanes' element-aligned vectors there): codes
+    bit-exact, padding untouched."""
     print(f"case: stochastic p/g views offset={offset} storage={storage} bits={bits} B={B} grad={gdt}",
           flush=True)
     rng = np.random.default_rng(42_000 + 10 * offset + B + storage)
