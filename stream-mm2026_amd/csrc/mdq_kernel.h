@@ -1397,18 +1397,19 @@ __device__ __forceinline__ void mdq_step_tile_any(const MdqDesc &d, long long ti
 // the register file never holds 8 of these waves, whatever the compiler's count.  With one
 // contiguous eighth of the tiles per XCD, 8 waves ran the LLaMA 4-bit step 1 % slower
 // (same-allocation A/B 13.36 vs 13.23 ms); with the chunked tile order the two are level
-// (+-0.3 %).  Steady steps on int8 + uint8 codes, and on packed 4-bit codes with nearest
-// rounding, are capped at 6 (v0..v79 reserved): their waves spend most of a tile waiting for its
-// loads, and one wave fewer per SIMD contends less.  Same-allocation A/B, nearest rounding:
-// 8-bit config 5 B = 64 / 128 / 256 -2.0 / -1.9 / -1.3 %, as packed views B = 128 -1.6 %,
-// LLaMA-7B -0.7 %; 4-bit (three boxes) LLaMA-7B -0.3 to -0.6 %, GPT-2 small -0.3 %, config 5
-// B = 64 -1.0 %, as packed views B = 128 -2.2 to -2.7 %.  Packed 4-bit codes with stochastic
-// rounding keep 7 (6: LLaMA-7B +0.8 %, views B = 64 +1.2 %); the stochastic 8-bit kernels need
-// 74-77 VGPRs and hold 6 anyway.
+// (+-0.3 %).  Steps on int8 + uint8 codes, and with nearest rounding steps on packed 4-bit
+// codes and storage-changing steps, are capped at 6 (v0..v79 reserved): their waves spend most
+// of a tile waiting for its loads, and one wave fewer per SIMD contends less.  Same-allocation
+// A/B, nearest rounding: 8-bit config 5 B = 64 / 128 / 256 -2.0 / -1.9 / -1.3 %, as packed views
+// B = 128 -1.6 %, LLaMA-7B -0.7 %; 4-bit (three boxes) LLaMA-7B -0.3 to -0.6 %, GPT-2 small
+// -0.3 %, config 5 B = 64 -1.0 %, as packed views B = 128 -2.2 to -2.7 %; storage changes on
+// the LLaMA-7B set 8 -> 16 -3.0 %, 4 -> 8 -1.9 %, 16 -> 4 -2.5 %, 16 -> 8 -0.7 %.  Packed
+// 4-bit codes with stochastic rounding keep 7 (6: LLaMA-7B +0.8 %, views B = 64 +1.2 %); most
+// other stochastic kernels need 73-85 VGPRs and hold 5-6 anyway.
 template <int SRC, int DST, bool SR>
 __device__ __forceinline__ void occupancy_cap()
 {
-    if constexpr ((SRC == ST_S8 && DST == ST_S8) || (SRC == ST_P4 && DST == ST_P4 && !SR)) asm volatile("" ::: "v79");
+    if constexpr ((SRC == ST_S8 && DST == ST_S8) || (!SR && (SRC == ST_P4 || SRC != DST))) asm volatile("" ::: "v79");
     else asm volatile("" ::: "v71");
 }
 
