@@ -396,16 +396,21 @@ def test_determinism_across_calls():
         assert torch.equal(a, b)
 
 
-def test_profile_cycles_accumulate():
+@pytest.mark.parametrize("tensors", [1, 2], ids=["one-tensor kernel", "descriptor-table kernel"])
+def test_profile_cycles_accumulate(tensors):
+    """All five phase sums grow, in the one-tensor launch (descriptor as a kernel argument) and in
+    a launch over a descriptor table; the steps stay exact."""
     rng = np.random.default_rng(9)
     n, B = 128 * 1000, 128
-    c = Case(n, B, orc.STORE_P4, rng)
-    g, tg = c.grads(rng)
+    cases = [Case(n + 384 * k, B, orc.STORE_P4, rng) for k in range(tensors)]
+    grads = [c.grads(rng) for c in cases]
     prof = torch.zeros(5, dtype=torch.int64, device=DEV)
-    mdq_hip.multi_tensor_step([c.entry(tg, 1, 4)], B, profile_cycles=prof)
-    p_prev = c.p.copy()
-    c.oracle_step(g, 1, 4)
-    c.check(p_prev)
+    mdq_hip.multi_tensor_step([c.entry(tg, 1, 4, tensor_id=k) for k, (c, (_g, tg)) in enumerate(zip(cases, grads))],
+                              B, profile_cycles=prof)
+    for k, (c, (g, _tg)) in enumerate(zip(cases, grads)):
+        p_prev = c.p.copy()
+        c.oracle_step(g, 1, 4, tensor_id=k)
+        c.check(p_prev)
     cyc = prof.cpu().numpy()
     assert np.all(cyc > 0), cyc
 
