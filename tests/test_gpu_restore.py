@@ -56,14 +56,21 @@ def src_state(src, n, B, rng):
 class Tensors:
     """Device tensors of one call; ``clone()`` gives an independent copy for the other route."""
 
-    def __init__(self, src, B, gdt, seed):
+    def __init__(self, src, B, gdt, seed, sizes=SIZES, offsets=None):
+        """``offsets``: per tensor, the element offsets of the p and grad views in their buffers
+        (default: p of the last tensor at 1, everything else at 0)."""
         rng = np.random.default_rng(seed)
+        if offsets is None:
+            offsets = [(1 if k == len(sizes) - 1 else 0, 0) for k in range(len(sizes))]
         self.items = []
-        for k, n in enumerate(SIZES):
+        for n, (off, goff) in zip(sizes, offsets):
             cm, cv, sm, sv, vm = src_state(src, n, B, rng)
-            off = 1 if k == len(SIZES) - 1 else 0
             pbuf = torch.from_numpy((rng.standard_normal(n + off) * 0.02).astype(np.float32)).to(DEV)
             g = torch.from_numpy((rng.standard_normal(n) * 1e-3).astype(np.float32)).to(DEV).to(GDT[gdt])
+            if goff:
+                gbuf = torch.zeros(n + goff, dtype=g.dtype, device=DEV)
+                gbuf[goff:] = g
+                g = gbuf[goff:]
             self.items.append([pbuf[off:], g, cm.to(DEV), cv.to(DEV), *(torch.from_numpy(a).to(DEV) for a in (sm, sv, vm))])
 
     def clone(self):
@@ -128,6 +135,32 @@ def test_restore_matches_separate_passes(src, dst, B):
         b = a.clone()
         separate_passes(a, dst, B, rounding, 99, step=7)
         fused(b, dst, B, rounding, 99, step=7)
+        assert_same(a, b, tag)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_restore_random_sweep(seed):
+    """Seeded random cases crossing the axes above: storage pair, B, rounding, grad dtype, one to
+    three tensors of random sizes (whole tiles and ragged tails), params and grads as views at
+    independent element offsets (inside a 128-byte line, 16-byte aligned or not), a random step."""
+    rng = np.random.default_rng(500 + seed)
+    for case in range(12):
+        src, dst = PAIRS[rng.integers(len(PAIRS))]
+        B = int(rng.choice([64, 128, 256]))
+        rounding = "stochastic" if rng.random() < 0.5 else "nearest"
+        gdt = str(rng.choice(list(GDT)))
+        k = int(rng.integers(1, 4))
+        sizes = [int(rng.integers(1, 40 * 512)) if rng.random() < 0.7 else 512 * int(rng.integers(1, 40))
+                 for _ in range(k)]
+        offsets = [(int(rng.choice([0, 0, 1, 4, 5, 16, 33])), int(rng.choice([0, 0, 2, 4, 8, 31]))) for _ in range(k)]
+        step = int(rng.integers(1, 50))
+        tag = (f"restore sweep seed={seed} #{case} {NAMES[src]} -> {NAMES[dst]} B={B} {gdt} {rounding} "
+               f"sizes={sizes} offsets={offsets} step={step}")
+        print(f"case: {tag}", flush=True)
+        a = Tensors(src, B, gdt, seed=10_000 * seed + case, sizes=sizes, offsets=offsets)
+        b = a.clone()
+        separate_passes(a, dst, B, rounding, 5, step=step)
+        fused(b, dst, B, rounding, 5, step=step)
         assert_same(a, b, tag)
 
 
