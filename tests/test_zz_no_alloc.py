@@ -64,6 +64,21 @@ def test_noalloc_matches_the_ordinary_entry_point(bits, rounding):
         print(f"call {call}: {len(sizes)} tensors, {sum(sizes):,} params bit-identical", flush=True)
 
 
+def test_noalloc_at_the_tensor_limit():
+    """Exactly STQ_NOALLOC_MAX_TENSORS tensors (the whole fixed descriptor array), sizes 1 to
+    2000 elements, then a call over 3 tensors; both bit-identical to the ordinary entry point."""
+    print(f"case: noalloc with {mdq_hip.NOALLOC_MAX_TENSORS} tensors", flush=True)
+    rng = np.random.default_rng(4096)
+    full = [int(x) for x in rng.integers(1, 2001, mdq_hip.NOALLOC_MAX_TENSORS)]
+    for call, sizes in enumerate((full, [300, 1, 70_000]), start=1):
+        ref, got = make_set(sizes, 4, 40 + call)
+        mdq_hip.MultiTensorPlan(entries(ref, 4, call), B).run()
+        mdq_hip.MultiTensorPlan(entries(got, 4, call), B).run(noalloc=True)
+        torch.cuda.synchronize()
+        _assert_same(ref, got, f"call {call}")
+        print(f"call {call}: {len(sizes)} tensors bit-identical", flush=True)
+
+
 def test_noalloc_refuses_too_many_tensors():
     ts = make_set([8] * (mdq_hip.NOALLOC_MAX_TENSORS + 1), 4, 0)[0]
     plan = mdq_hip.MultiTensorPlan(entries(ts, 4, 1), B)
