@@ -26,7 +26,7 @@ OFFSETS = [0, 0, 1, 3, 4, 5, 16, 31, 33]
 def _draw(rng, max_tiles):
     storage, bits = STORAGES[rng.integers(len(STORAGES))]
     B = int(2 ** rng.integers(0, 11))
-    stochastic = bool(rng.integers(2)) and bits <= 16
+    stochastic = bool(rng.integers(2))     # at 32 bits the step rounds to nearest either way
     gdt = GRAD_DTYPES[rng.integers(len(GRAD_DTYPES))]
     offset = int(rng.choice(OFFSETS))
     tiles = int(np.exp(rng.uniform(0, np.log(max_tiles))))
