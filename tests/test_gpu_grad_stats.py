@@ -57,6 +57,29 @@ def test_kernel_matches_oracle(dtype, offset):
             np.testing.assert_allclose(got[i], tr, rtol=1e-5, atol=0, err_msg=f"torch, tensor {i}")
 
 
+def test_thousands_of_small_tensors_one_launch():
+    """3000 grads of 1 to 5000 elements (log-uniform, some empty) in one launch: every row against
+    the oracle, and the launch deterministic."""
+    print("case: grad_stats over 3000 small tensors", flush=True)
+    rng = np.random.default_rng(3000)
+    sizes = np.floor(np.exp(rng.uniform(0, np.log(5000), 3000))).astype(int)
+    sizes[rng.random(3000) < 0.01] = 0
+    flat = torch.from_numpy((rng.standard_t(3, int(sizes.sum())) * 1e-3).astype(np.float32)).to(DEV)
+    vs, o = [], 0
+    for n in sizes:
+        vs.append(flat[o:o + int(n)])
+        o += int(n)
+    got = mdq_hip.grad_stats(vs).cpu().numpy()
+    again = mdq_hip.grad_stats(vs).cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32)), "not deterministic"
+    host = flat.cpu().numpy()
+    o = 0
+    for i, n in enumerate(sizes):
+        ref = orc.grad_stats(host[o:o + int(n)])
+        o += int(n)
+        np.testing.assert_allclose(got[i], ref, rtol=1e-6, atol=0, equal_nan=True, err_msg=f"tensor {i} n={n}")
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_nonfinite_grads_match_oracle(dtype):
     """NaN, +-inf and (fp32) overflowing squares in some tensors of a launch: the kernel gives the
