@@ -67,6 +67,29 @@ def test_align_matches_reference(src, bits):
         assert np.array_equal(as_i64(nv.cpu()).numpy(), v), f"v codes, n={n}"
 
 
+@pytest.mark.parametrize("src,bits", [("s16", 4), ("p4", 8), ("s8", 16)])
+def test_thousands_of_small_tensors_one_launch(src, bits):
+    """2000 tensors of 1 to 3000 elements (log-uniform) aligned in one launch, the usual
+    transitions of the MDQ schedule: every tensor against the storage model."""
+    print(f"case: convert 2000 tensors {src} -> bits {bits}", flush=True)
+    rng = np.random.default_rng(2000 + bits)
+    sizes = [int(x) for x in np.floor(np.exp(rng.uniform(0, np.log(3000), 2000)))]
+    items, states, want = [], [], []
+    for k, n in enumerate(sizes):
+        cm, cv = rand_codes(src, n, 9000 + k)
+        want.append(_model(before_kernel, src, cm, cv, bits))
+        gm, gv = cm.to(DEV), cv.to(DEV)
+        nm, nv = mdq_hip.empty_codes(gm, storage.kernel_layout(bits))
+        items.append((gm, gv, nm, nv))
+        states.append((nm, nv))
+    mdq_hip.convert_codes(items)
+    torch.cuda.synchronize()
+    for k, ((nm, nv), (lay, m, v)) in enumerate(zip(states, want)):
+        assert storage.layout_of(nm, nv) == lay, (k, nm.dtype, nv.dtype)
+        assert np.array_equal(as_i64(nm.cpu()).numpy(), m), f"m codes, tensor {k}"
+        assert np.array_equal(as_i64(nv.cpu()).numpy(), v), f"v codes, tensor {k}"
+
+
 def test_pack_to_nibbles_matches_reference():
     items, want, outs = [], [], []
     for k, n in enumerate(SIZES):
