@@ -164,6 +164,21 @@ def test_restore_random_sweep(seed):
         assert_same(a, b, tag)
 
 
+@pytest.mark.parametrize("src,dst", [(mdq_hip.STORE_S16, mdq_hip.STORE_P4), (mdq_hip.STORE_S8, mdq_hip.STORE_S16)],
+                         ids=["s16-p4", "s8-s16"])
+def test_restore_thousands_of_small_tensors(src, dst):
+    """1500 tensors of 1 to 3000 elements (log-uniform) changing storage in one launch (a
+    1500-entry descriptor table), against the separate passes."""
+    print(f"case: restore 1500 tensors {NAMES[src]} -> {NAMES[dst]}", flush=True)
+    rng = np.random.default_rng(1500 + src)
+    sizes = [int(x) for x in np.floor(np.exp(rng.uniform(0, np.log(3000), 1500)))]
+    a = Tensors(src, 128, "bf16", seed=77, sizes=sizes, offsets=[(0, 0)] * len(sizes))
+    b = a.clone()
+    separate_passes(a, dst, 128, "nearest", 3, step=9)
+    fused(b, dst, 128, "nearest", 3, step=9)
+    assert_same(a, b, f"restore 1500 tensors {NAMES[src]} -> {NAMES[dst]}")
+
+
 @pytest.mark.parametrize("cls", [MDQAdamWSimple, MDQAdamWSimpleFusedIO])
 @pytest.mark.parametrize("B", [64, 256, 512])
 def test_optimizer_fused_transitions_match_separate_passes(cls, B):
